@@ -1,0 +1,97 @@
+// Shared device helpers for the gfx950 kernels behind include/mi_qmm.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mi_qmm.h"
+
+namespace mi {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Error reporting (mi_abi.hip). fail() records the message and returns code.
+int fail(int code, const char *fmt, ...);
+int launch_status(const char *what);  // MI_OK or MI_ERR_LAUNCH after a launch
+
+// 8 lanes of T packed in 16 bytes, and 4 lanes in 8 bytes.
+template <typename T> struct Vec;
+template <> struct Vec<bf16> { typedef bf16x8 x8; typedef bf16x4 x4; };
+template <> struct Vec<f16> { typedef f16x8 x8; typedef f16x4 x4; };
+
+template <typename T> __device__ __forceinline__ float f32(T v) { return (float)v; }
+// float -> T with one round-to-nearest-even conversion (v_cvt_pk_bf16_f32 /
+// v_cvt_f16_f32 on gfx950).
+template <typename T> __device__ __forceinline__ T cvt(float v) { return (T)v; }
+
+__device__ __forceinline__ uint4 ld16(const void *p) { return *(const uint4 *)p; }
+__device__ __forceinline__ uint2 ld8(const void *p) { return *(const uint2 *)p; }
+__device__ __forceinline__ void st16(void *p, uint4 v) { *(uint4 *)p = v; }
+__device__ __forceinline__ void st8(void *p, uint2 v) { *(uint2 *)p = v; }
+
+// Unpack the 8 values of a 16-byte group of T into floats.
+template <typename T> __device__ __forceinline__ void unpack8(uint4 raw, float (&f)[8]) {
+    typedef typename Vec<T>::x8 V;
+    V v = __builtin_bit_cast(V, raw);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = (float)v[i];
+}
+
+template <typename T> __device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
+    typedef typename Vec<T>::x8 V;
+    V v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (T)f[i];
+    return __builtin_bit_cast(uint4, v);
+}
+
+template <typename T> __device__ __forceinline__ uint2 pack4(const float (&f)[4]) {
+    typedef typename Vec<T>::x4 V;
+    V v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = (T)f[i];
+    return __builtin_bit_cast(uint2, v);
+}
+
+// Affine dequant of the 8 consecutive values starting at nibble/byte `first`
+// of a packed chunk: T(fma(s, q, b)), one rounding (the reference's dequant
+// form). For 4 bits the 8 values are the 8 nibbles of word w0; for 8 bits
+// they are the 4 bytes of w0 followed by the 4 bytes of w1.
+template <typename T, int BITS>
+__device__ __forceinline__ typename Vec<T>::x8 dequant8(uint32_t w0, uint32_t w1, float s,
+                                                       float b) {
+    typename Vec<T>::x8 r;
+    if constexpr (BITS == 4) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            r[i] = (T)__builtin_fmaf(s, (float)((w0 >> (4 * i)) & 15u), b);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            r[i] = (T)__builtin_fmaf(s, (float)((w0 >> (8 * i)) & 255u), b);
+            r[4 + i] = (T)__builtin_fmaf(s, (float)((w1 >> (8 * i)) & 255u), b);
+        }
+    }
+    return r;
+}
+
+__host__ __device__ constexpr int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline hipStream_t as_stream(void *s) { return (hipStream_t)s; }
+
+inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+inline bool valid_dtype(int d) { return d == MI_F32 || d == MI_F16 || d == MI_BF16; }
+
+// Checks shared by the quantized entries (scaffold/stitch.py:103-123).
+int check_quant(int64_t N, int64_t K, int group_size, int bits, int dtype);
+
+}  // namespace mi

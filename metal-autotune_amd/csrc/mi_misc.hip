@@ -1,0 +1,218 @@
+// Rows A8 (SwiGLU), A9 (LFM2 short-conv core), A10 (fp32 linear + exact GELU
+// for the tiny-MLP region) and the greedy-argmax glue of A12. All HBM- or
+// launch-bound elementwise/row work: 16-byte vector loads where the layout
+// allows, one thread per 8 values.
+#include <math.h>
+
+#include "mi_common.h"
+
+namespace mi {
+namespace {
+
+template <typename T> __device__ __forceinline__ float swiglu_one(float g, float u) {
+    const float sig = (float)cvt<T>(1.0f / (1.0f + __expf(-g)));
+    const float act = (float)cvt<T>(g * sig);
+    return act * u;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_kernel(const T *__restrict__ g,
+                                                     const T *__restrict__ u, T *__restrict__ y,
+                                                     int64_t n, int vec_ok) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if constexpr (sizeof(T) == 2) {
+        if (vec_ok) {
+            if (t * 8 >= n) return;
+            float gf[8], uf[8];
+            unpack8<T>(ld16(g + 8 * t), gf);
+            unpack8<T>(ld16(u + 8 * t), uf);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) gf[i] = swiglu_one<T>(gf[i], uf[i]);
+            st16(y + 8 * t, pack8<T>(gf));
+            return;
+        }
+    }
+    for (int64_t i = t * 8; i < n && i < t * 8 + 8; ++i)
+        y[i] = cvt<T>(swiglu_one<T>((float)g[i], (float)u[i]));
+}
+
+// Grid rows 0..L-1 produce out; rows L, L+1 copy the last two padded rows into
+// state_out. pad[i] = state_in[i] (or 0) for i < 2, bx[i-2] otherwise.
+template <typename T>
+__global__ __launch_bounds__(256) void shortconv_kernel(const T *__restrict__ bx,
+                                                        const T *__restrict__ c,
+                                                        const T *__restrict__ w,
+                                                        const T *__restrict__ st_in,
+                                                        T *__restrict__ out,
+                                                        T *__restrict__ st_out, int64_t B,
+                                                        int64_t L, int64_t D) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t dchunks = ceil_div(D, 8);
+    if (t >= B * (L + 2) * dchunks) return;
+    const int64_t dc = t % dchunks, row = (t / dchunks) % (L + 2), b = t / (dchunks * (L + 2));
+    auto pad = [&](int64_t i, int64_t d) -> float {
+        if (i >= 2) return (float)bx[(b * L + i - 2) * D + d];
+        return st_in ? (float)st_in[(b * 2 + i) * D + d] : 0.0f;
+    };
+    for (int64_t d = dc * 8; d < D && d < dc * 8 + 8; ++d) {
+        if (row < L) {
+            float acc = pad(row, d) * (float)w[d * 3 + 0];
+            acc = __builtin_fmaf(pad(row + 1, d), (float)w[d * 3 + 1], acc);
+            acc = __builtin_fmaf(pad(row + 2, d), (float)w[d * 3 + 2], acc);
+            const float conv = (float)cvt<T>(acc);
+            out[(b * L + row) * D + d] = cvt<T>((float)c[(b * L + row) * D + d] * conv);
+        } else if (st_out) {
+            const int64_t i = row - L;  // 0 or 1
+            st_out[(b * 2 + i) * D + d] = cvt<T>(pad(L + i, d));
+        }
+    }
+}
+
+// fp32 linear: 16x16 output tile per 256-thread block, K in 16-wide LDS tiles,
+// each output's sum sequential in k.
+__global__ __launch_bounds__(256) void linear_f32_kernel(const float *__restrict__ x,
+                                                         const float *__restrict__ w,
+                                                         const float *__restrict__ bias,
+                                                         float *__restrict__ y, int64_t M,
+                                                         int64_t N, int64_t K, int act) {
+    __shared__ float xs[16][17];
+    __shared__ float ws[16][17];
+    const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+    const int64_t n = (int64_t)blockIdx.x * 16 + tx;
+    const int64_t m = (int64_t)blockIdx.y * 16 + ty;
+    float acc = 0.0f;
+    for (int64_t k0 = 0; k0 < K; k0 += 16) {
+        const int64_t xm = (int64_t)blockIdx.y * 16 + ty, wn = (int64_t)blockIdx.x * 16 + ty;
+        xs[ty][tx] = (xm < M && k0 + tx < K) ? x[xm * K + k0 + tx] : 0.0f;
+        ws[ty][tx] = (wn < N && k0 + tx < K) ? w[wn * K + k0 + tx] : 0.0f;
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) acc = __builtin_fmaf(xs[ty][kk], ws[tx][kk], acc);
+        __syncthreads();
+    }
+    if (m >= M || n >= N) return;
+    if (bias) acc += bias[n];
+    if (act == MI_ACT_GELU) acc = acc * (1.0f + erff(acc / 1.41421356237f)) / 2.0f;
+    y[m * N + n] = acc;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void argmax_kernel(const T *__restrict__ x,
+                                                     int32_t *__restrict__ out, int64_t V) {
+    __shared__ float sv[4];
+    __shared__ int64_t si[4];
+    const T *row = x + (int64_t)blockIdx.x * V;
+    float best = -INFINITY;
+    int64_t bi = -1;
+    for (int64_t i = threadIdx.x; i < V; i += 256) {
+        const float v = (float)row[i];
+        if (v > best || (bi < 0 && !isnan(v))) {
+            best = v;
+            bi = i;
+        }
+    }
+    // (value, index) max with lowest index on ties; -1 = no candidate
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int64_t oi = __shfl_xor(bi, o, 64);
+        if (oi >= 0 && (bi < 0 || ov > best || (ov == best && oi < bi))) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sv[wave] = best;
+        si[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w2 = 1; w2 < 4; ++w2)
+            if (si[w2] >= 0 && (bi < 0 || sv[w2] > best || (sv[w2] == best && si[w2] < bi))) {
+                best = sv[w2];
+                bi = si[w2];
+            }
+        out[blockIdx.x] = (int32_t)(bi < 0 ? 0 : bi);
+    }
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int mi_swiglu(const void *g, const void *u, void *y, int64_t n, int dtype,
+                         void *stream) {
+    if (!valid_dtype(dtype)) return fail(MI_ERR_UNSUPPORTED, "dtype code %d", dtype);
+    if (n < 0) return fail(MI_ERR_ARG, "negative size");
+    if (n == 0) return MI_OK;
+    if (!g || !u || !y) return fail(MI_ERR_ARG, "null pointer");
+    hipStream_t st = as_stream(stream);
+    const unsigned grid = (unsigned)ceil_div(ceil_div(n, 8), 256);
+    const int vec = n % 8 == 0 && aligned(g, 16) && aligned(u, 16) && aligned(y, 16);
+    if (dtype == MI_BF16)
+        swiglu_kernel<bf16><<<grid, 256, 0, st>>>((const bf16 *)g, (const bf16 *)u, (bf16 *)y, n,
+                                                  vec);
+    else if (dtype == MI_F16)
+        swiglu_kernel<f16><<<grid, 256, 0, st>>>((const f16 *)g, (const f16 *)u, (f16 *)y, n,
+                                                 vec);
+    else
+        swiglu_kernel<float><<<grid, 256, 0, st>>>((const float *)g, (const float *)u,
+                                                    (float *)y, n, vec);
+    return launch_status("swiglu");
+}
+
+extern "C" int mi_shortconv(const void *bx, const void *c, const void *w, const void *state_in,
+                            void *out, void *state_out, int64_t B, int64_t L, int64_t D,
+                            int dtype, void *stream) {
+    if (!valid_dtype(dtype)) return fail(MI_ERR_UNSUPPORTED, "dtype code %d", dtype);
+    if (B < 0 || L < 0 || D <= 0) return fail(MI_ERR_ARG, "shortconv shape");
+    if (state_out && (state_out == state_in || state_out == bx || state_out == c))
+        return fail(MI_ERR_ARG, "state_out must not alias an input");
+    if (B * L && (!bx || !c || !w || !out)) return fail(MI_ERR_ARG, "null pointer");
+    const int64_t threads = B * (L + 2) * ceil_div(D, 8);
+    if (threads == 0) return MI_OK;
+    hipStream_t st = as_stream(stream);
+    const unsigned grid = (unsigned)ceil_div(threads, 256);
+#define MI_SC(TT)                                                                               \
+    shortconv_kernel<TT><<<grid, 256, 0, st>>>((const TT *)bx, (const TT *)c, (const TT *)w,    \
+                                               (const TT *)state_in, (TT *)out, (TT *)state_out, \
+                                               B, L, D)
+    if (dtype == MI_BF16)
+        MI_SC(bf16);
+    else if (dtype == MI_F16)
+        MI_SC(f16);
+    else
+        MI_SC(float);
+#undef MI_SC
+    return launch_status("shortconv");
+}
+
+extern "C" int mi_linear_f32(const float *x, const float *w, const float *bias, float *y,
+                             int64_t M, int64_t N, int64_t K, int act, void *stream) {
+    if (M < 0 || N < 0 || K <= 0) return fail(MI_ERR_ARG, "linear shape");
+    if (act != MI_ACT_NONE && act != MI_ACT_GELU)
+        return fail(MI_ERR_UNSUPPORTED, "linear activation %d", act);
+    if (M == 0 || N == 0) return MI_OK;
+    if (!x || !w || !y) return fail(MI_ERR_ARG, "null pointer");
+    const dim3 grid((unsigned)ceil_div(N, 16), (unsigned)ceil_div(M, 16));
+    linear_f32_kernel<<<grid, 256, 0, as_stream(stream)>>>(x, w, bias, y, M, N, K, act);
+    return launch_status("linear_f32");
+}
+
+extern "C" int mi_argmax(const void *x, int32_t *out, int64_t rows, int64_t V, int dtype,
+                         void *stream) {
+    if (!valid_dtype(dtype)) return fail(MI_ERR_UNSUPPORTED, "dtype code %d", dtype);
+    if (rows < 0 || V <= 0) return fail(MI_ERR_ARG, "argmax shape");
+    if (rows == 0) return MI_OK;
+    if (!x || !out) return fail(MI_ERR_ARG, "null pointer");
+    hipStream_t st = as_stream(stream);
+    if (dtype == MI_BF16)
+        argmax_kernel<bf16><<<(unsigned)rows, 256, 0, st>>>((const bf16 *)x, out, V);
+    else if (dtype == MI_F16)
+        argmax_kernel<f16><<<(unsigned)rows, 256, 0, st>>>((const f16 *)x, out, V);
+    else
+        argmax_kernel<float><<<(unsigned)rows, 256, 0, st>>>((const float *)x, out, V);
+    return launch_status("argmax");
+}

@@ -1,0 +1,227 @@
+// Rows A5 (RMSNorm, and the [qmm, add, rms_norm] region) and A6 (q/k-norm + RoPE).
+//
+// Both are HBM/launch-bound single-pass wave reductions: one wave (or a
+// power-of-two lane group) owns a row, sums squares in fp32 with an xor-shuffle
+// tree, and writes T(w * T(x * inv)) -- the two-rounding form the reference's
+// exact-verified LFM2 norm stage uses (prefill_bk64.stages/1.metal:34-42).
+#include <math.h>
+
+#include "mi_common.h"
+
+namespace mi {
+int qmm_residual_launch(const void *x, const uint32_t *w, const void *s, const void *b,
+                        const void *resid, void *y, int64_t M, int64_t N, int64_t K, int gs,
+                        int bits, int dtype, void *stream);
+
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void rms_kernel(const T *__restrict__ x, const T *__restrict__ w,
+                                                  T *__restrict__ y, int64_t rows, int64_t D,
+                                                  float eps, int vec_ok) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const T *xr = x + row * D;
+    T *yr = y + row * D;
+    float ss = 0.0f;
+    const bool vec = (sizeof(T) == 2) && vec_ok;
+    if (vec) {
+        for (int64_t c = lane; c < D / 8; c += 64) {
+            float f[8];
+            if constexpr (sizeof(T) == 2) unpack8<T>(ld16(xr + 8 * c), f);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(f[i], f[i], ss);
+        }
+    } else {
+        for (int64_t k = lane; k < D; k += 64) {
+            const float v = (float)xr[k];
+            ss = __builtin_fmaf(v, v, ss);
+        }
+    }
+    ss = wave_sum(ss);
+    const float inv = 1.0f / __fsqrt_rn(ss / (float)D + eps);
+    if (vec) {
+        for (int64_t c = lane; c < D / 8; c += 64) {
+            if constexpr (sizeof(T) == 2) {
+                float f[8], g[8];
+                unpack8<T>(ld16(xr + 8 * c), f);
+                unpack8<T>(ld16(w + 8 * c), g);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) f[i] = g[i] * (float)cvt<T>(f[i] * inv);
+                st16(yr + 8 * c, pack8<T>(f));
+            }
+        }
+    } else {
+        for (int64_t k = lane; k < D; k += 64)
+            yr[k] = cvt<T>((float)w[k] * (float)cvt<T>((float)xr[k] * inv));
+    }
+}
+
+template <typename T>
+int launch_rms(const void *x, const void *w, void *y, int64_t rows, int64_t D, float eps,
+               hipStream_t st) {
+    if (rows == 0) return MI_OK;
+    const int vec = D % 8 == 0 && aligned(x, 16) && aligned(w, 16) && aligned(y, 16);
+    rms_kernel<T><<<(unsigned)ceil_div(rows, 4), 256, 0, st>>>((const T *)x, (const T *)w,
+                                                                (T *)y, rows, D, eps, vec);
+    return launch_status("rms_norm");
+}
+
+// One row = one head vector of D values, owned by R lanes (R a power of two).
+// Slot p < dims/2 is a rotated pair; slots past it copy two tail values.
+template <typename T, int R>
+__global__ __launch_bounds__(256) void norm_rope_kernel(
+    const T *__restrict__ x, const T *__restrict__ w, T *__restrict__ out, int64_t B, int64_t L,
+    int64_t H, int64_t D, int64_t xs, float eps, int dims, int trad, float log2base,
+    float scale, int64_t offset, int64_t cap, int64_t pos0) {
+    const int t = threadIdx.x % R;
+    const int64_t row = (int64_t)blockIdx.x * (256 / R) + threadIdx.x / R;
+    if (row >= B * L * H) return;
+    const int64_t h = row % H, l = (row / H) % L, b = row / (H * L);
+    const T *xr = x + (b * L + l) * xs + h * D;
+    T *orow = out + ((b * H + h) * cap + pos0 + l) * D;
+    const int half = dims / 2;
+    const int slots = (int)(D / 2);
+    float inv = 1.0f;
+    if (w) {
+        float ss = 0.0f;
+        for (int k = t; k < D; k += R) {
+            const float v = (float)xr[k];
+            ss = __builtin_fmaf(v, v, ss);
+        }
+#pragma unroll
+        for (int o = R / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, R);
+        inv = 1.0f / __fsqrt_rn(ss / (float)D + eps);
+    }
+    const float position = (float)(l + offset) * scale;
+    for (int p = t; p < slots; p += R) {
+        int e0, e1;
+        const bool rot = p < half;
+        if (trad || !rot) {
+            e0 = rot ? 2 * p : dims + 2 * (p - half);
+            e1 = e0 + 1;
+        } else {
+            e0 = p;
+            e1 = p + half;
+        }
+        float a = (float)xr[e0], c = (float)xr[e1];
+        if (w) {
+            a = (float)cvt<T>((float)w[e0] * (float)cvt<T>(a * inv));
+            c = (float)cvt<T>((float)w[e1] * (float)cvt<T>(c * inv));
+        }
+        if (rot) {
+            const float inv_freq = exp2f(-(float)(2 * p) / (float)dims * log2base);
+            float sn, cs;
+            sincosf(position * inv_freq, &sn, &cs);
+            const float ra = a * cs - c * sn;
+            const float rc = a * sn + c * cs;
+            a = ra;
+            c = rc;
+        }
+        orow[e0] = cvt<T>(a);
+        orow[e1] = cvt<T>(c);
+    }
+}
+
+template <typename T>
+int launch_norm_rope(const void *x, const void *w, void *out, int64_t B, int64_t L, int64_t H,
+                     int64_t D, int64_t xs, float eps, int dims, int trad, float log2base,
+                     float scale, int64_t offset, int64_t cap, int64_t pos0, hipStream_t st) {
+    const int64_t rows = B * L * H;
+    if (rows == 0) return MI_OK;
+    const int64_t slots = D / 2;
+#define MI_NR_LAUNCH(RR)                                                                       \
+    norm_rope_kernel<T, RR><<<(unsigned)ceil_div(rows, 256 / RR), 256, 0, st>>>(                \
+        (const T *)x, (const T *)w, (T *)out, B, L, H, D, xs, eps, dims, trad, log2base, scale, \
+        offset, cap, pos0)
+    if (slots >= 64)
+        MI_NR_LAUNCH(64);
+    else if (slots >= 32)
+        MI_NR_LAUNCH(32);
+    else if (slots >= 16)
+        MI_NR_LAUNCH(16);
+    else
+        MI_NR_LAUNCH(8);
+#undef MI_NR_LAUNCH
+    return launch_status("norm_rope");
+}
+
+}  // namespace
+
+int rms_launch(const void *x, const void *w, void *y, int64_t rows, int64_t D, float eps,
+               int dtype, void *stream) {
+    if (!valid_dtype(dtype)) return fail(MI_ERR_UNSUPPORTED, "dtype code %d", dtype);
+    if (rows < 0 || D <= 0) return fail(MI_ERR_ARG, "rms_norm shape rows=%lld D=%lld",
+                                        (long long)rows, (long long)D);
+    if (rows && (!x || !w || !y)) return fail(MI_ERR_ARG, "null pointer");
+    hipStream_t st = as_stream(stream);
+    switch (dtype) {
+    case MI_BF16: return launch_rms<bf16>(x, w, y, rows, D, eps, st);
+    case MI_F16: return launch_rms<f16>(x, w, y, rows, D, eps, st);
+    default: return launch_rms<float>(x, w, y, rows, D, eps, st);
+    }
+}
+
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int mi_rms_norm(const void *x, const void *w, void *y, int64_t rows, int64_t D,
+                           float eps, int dtype, void *stream) {
+    return rms_launch(x, w, y, rows, D, eps, dtype, stream);
+}
+
+extern "C" int mi_qmm_affine_residual_rmsnorm(const void *x, const uint32_t *w,
+                                              const void *scales, const void *biases,
+                                              const void *resid, const void *norm_w, float eps,
+                                              void *h, void *y, int64_t M, int64_t N, int64_t K,
+                                              int group_size, int bits, int dtype,
+                                              void *stream) {
+    if (M && N && (!norm_w || !y)) return fail(MI_ERR_ARG, "null norm weight or output");
+    if (int e = qmm_residual_launch(x, w, scales, biases, resid, h, M, N, K, group_size, bits,
+                                    dtype, stream))
+        return e;
+    if (M == 0 || N == 0) return MI_OK;
+    return rms_launch(h, norm_w, y, M, N, eps, dtype, stream);
+}
+
+extern "C" int mi_norm_rope(const void *x, const void *w, void *out, int64_t B, int64_t L,
+                            int64_t H, int64_t D, int64_t x_row_stride, float eps, int rope_dims,
+                            int traditional, float base, float scale, int64_t offset,
+                            int64_t out_seq_cap, int64_t out_pos, int dtype, void *stream) {
+    if (!valid_dtype(dtype)) return fail(MI_ERR_UNSUPPORTED, "dtype code %d", dtype);
+    if (B < 0 || L < 0 || H <= 0 || D <= 0 || D % 2)
+        return fail(MI_ERR_ARG, "norm_rope shape B=%lld L=%lld H=%lld D=%lld", (long long)B,
+                    (long long)L, (long long)H, (long long)D);
+    if (rope_dims < 0 || rope_dims > D || rope_dims % 2)
+        return fail(MI_ERR_ARG, "rope dims %d vs head dim %lld", rope_dims, (long long)D);
+    if (x_row_stride < H * D) return fail(MI_ERR_ARG, "x row stride smaller than H*D");
+    if (out_pos < 0 || out_pos + L > out_seq_cap)
+        return fail(MI_ERR_ARG, "rows [%lld, %lld) exceed the output capacity %lld",
+                    (long long)out_pos, (long long)(out_pos + L), (long long)out_seq_cap);
+    if (rope_dims && !(base > 0.0f)) return fail(MI_ERR_ARG, "rope base must be positive");
+    if (B * L && (!x || !out)) return fail(MI_ERR_ARG, "null pointer");
+    const float log2base = rope_dims ? (float)log2((double)base) : 0.0f;
+    hipStream_t st = as_stream(stream);
+    switch (dtype) {
+    case MI_BF16:
+        return launch_norm_rope<bf16>(x, w, out, B, L, H, D, x_row_stride, eps, rope_dims,
+                                      traditional, log2base, scale, offset, out_seq_cap, out_pos,
+                                      st);
+    case MI_F16:
+        return launch_norm_rope<f16>(x, w, out, B, L, H, D, x_row_stride, eps, rope_dims,
+                                     traditional, log2base, scale, offset, out_seq_cap, out_pos,
+                                     st);
+    default:
+        return launch_norm_rope<float>(x, w, out, B, L, H, D, x_row_stride, eps, rope_dims,
+                                       traditional, log2base, scale, offset, out_seq_cap, out_pos,
+                                       st);
+    }
+}

@@ -1,0 +1,76 @@
+"""The C-ABI library: it loads, exports every symbol include/mi_qmm.h declares,
+and the Python binding table covers exactly those symbols. CPU only (no compute
+calls). Also: no product module imports the oracle."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "mi_qmm.h"
+LIB = ROOT / "metal-autotune_amd" / "libmiqmm.so"
+
+
+def declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mi_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = declared_symbols()
+    for want in ("mi_qmm_affine", "mi_affine_dequant", "mi_sdpa", "mi_last_error", "mi_abi_version"):
+        assert want in names
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not LIB.exists():
+        pytest.fail(f"{LIB} is not built: run __graft_entry__.build()")
+    return ctypes.CDLL(str(LIB))
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [n for n in declared_symbols() if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+
+
+def test_abi_version_and_error_string(lib):
+    lib.mi_abi_version.restype = ctypes.c_int
+    lib.mi_last_error.restype = ctypes.c_char_p
+    assert lib.mi_abi_version() == 1
+    assert isinstance(lib.mi_last_error(), bytes)
+
+
+def test_argument_errors_need_no_device(lib):
+    """Shape/dtype checks run before any HIP call: a bad call returns
+    MI_ERR_ARG / MI_ERR_UNSUPPORTED with a message, on the CPU."""
+    lib.mi_qmm_affine.restype = ctypes.c_int
+    lib.mi_last_error.restype = ctypes.c_char_p
+    P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.mi_qmm_affine.argtypes = [P, P, P, P, P, I64, I64, I64, I, I, I, P]
+    assert lib.mi_qmm_affine(None, None, None, None, None, 1, 8, 100, 64, 4, 2, None) == 1
+    assert b"multiple of group_size" in lib.mi_last_error()
+    assert lib.mi_qmm_affine(None, None, None, None, None, 1, 8, 128, 64, 3, 2, None) == 2
+    assert lib.mi_qmm_affine(None, None, None, None, None, 1, 8, 128, 48, 4, 2, None) == 2
+
+
+def test_binding_table_matches_header():
+    import sys
+    sys.path.insert(0, str(ROOT / "metal-autotune_amd"))
+    from autotuner_runtime import hip
+
+    assert sorted(hip.SIGNATURES) == declared_symbols()
+    assert set(hip.BINDINGS) <= set(hip.SIGNATURES)
+
+
+def test_product_code_never_imports_the_oracle():
+    for py in (ROOT / "metal-autotune_amd").rglob("*.py"):
+        text = py.read_text()
+        assert not re.search(r"^\s*(import|from)\s+oracle\b", text, flags=re.M), py
+    for src in (ROOT / "metal-autotune_amd" / "csrc").glob("*"):
+        assert "orc_" not in src.read_text(), src

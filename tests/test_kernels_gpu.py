@@ -1,0 +1,344 @@
+"""GPU parity of every HIP kernel against the CPU oracle, through the C ABI.
+
+Bars: bit-exact for dequant, integer/index outputs and the one-hot cases;
+otherwise the port's region criterion max|c - r| <= tol * max|r| with
+tol 1e-2 for bf16/fp16 and 1e-5 for fp32 (numeric.max_abs_normalised).
+Shapes are BASELINE config 2 (x[M, 2560] @ W[9728, 2560]^T, M in 1/16/128),
+the Qwen3/LFM2 projection shapes, and ragged edges.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import packed_to_torch, rng, to_np, to_torch
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+from autotuner_runtime import hip, numeric, ops  # noqa: E402
+
+
+def _close(got, want, dtype, tol=None):
+    t = numeric.max_abs_normalised(to_torch(got, dtype, "cpu") if isinstance(got, np.ndarray) else got.cpu(),
+                                   to_torch(want, dtype, "cpu"), tol)
+    assert t.passed, f"max-abs-normalised error {t.error:.3e} > {t.tol:.1e} ({t.detail})"
+    return t.error
+
+
+def _quant(seed, N, K, gs=64, bits=4, dtype="bfloat16"):
+    r = rng(seed)
+    return oracle.quantize_affine(r.normal(0, 0.02, (N, K)).astype(np.float32), gs, bits, dtype)
+
+
+def _dev(wq, s, b, dtype):
+    return packed_to_torch(wq), to_torch(s, dtype), to_torch(b, dtype)
+
+
+# ---------------------------------------------------------------------- A1
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("bits,gs", [(4, 64), (4, 32), (4, 128), (8, 64), (8, 128)])
+def test_dequant_bit_exact(dtype, bits, gs):
+    wq, s, b = _quant(100 + bits + gs, 96, 1024, gs, bits, dtype)
+    want = oracle.dequantize(wq, s, b, gs, bits, dtype)
+    got = ops.dequantize(*_dev(wq, s, b, dtype), group_size=gs, bits=bits)
+    assert np.array_equal(to_np(got).view(np.uint32), want.view(np.uint32))
+
+
+def test_dequant_config2_shape_bit_exact():
+    wq, s, b = _quant(7, 9728, 2560)
+    want = oracle.dequantize(wq, s, b, 64, 4, "bfloat16")
+    got = ops.dequantize(*_dev(wq, s, b, "bfloat16"))
+    assert np.array_equal(to_np(got).view(np.uint32), want.view(np.uint32))
+
+
+def test_quantized_embedding_gathers_dequantized_rows():
+    wq, s, b = _quant(8, 500, 256)
+    W = oracle.dequantize(wq, s, b, 64, 4, "bfloat16")
+    ids = np.array([[3, 0, 499, 3, 17]], np.int64)
+    for idt in (torch.int64, torch.int32):
+        got = ops.quantized_embedding(torch.from_numpy(ids).to("cuda", idt), *_dev(wq, s, b, "bfloat16"))
+        assert got.shape == (1, 5, 256)
+        assert np.array_equal(to_np(got)[0], W[ids[0]])
+
+
+# ------------------------------------------------------------------- A2-A4
+
+
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 9, 16, 33, 64, 100, 128, 300])
+def test_qmm_config2_shape(M):
+    """BASELINE config 2 shapes (M in 1/16/128) and the GEMV/MFMA switch
+    points around them."""
+    r = rng(200 + M)
+    K, N = 2560, 9728
+    x = oracle.round_to(r.normal(0, 1, (M, K)), "bfloat16")
+    wq, s, b = _quant(7, N, K)
+    y = ops.quantized_matmul(to_torch(x, "bfloat16"), *_dev(wq, s, b, "bfloat16"))
+    if M <= 16:
+        want = oracle.qmm_factored(x, wq, s, b, 64, 4, "bfloat16")
+    else:
+        want = oracle.quantized_matmul(x, wq, s, b, 64, 4, "bfloat16")
+    _close(y, want, "bfloat16")
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("bits,gs", [(4, 64), (8, 64), (4, 32), (4, 128), (8, 32)])
+@pytest.mark.parametrize("M", [1, 7, 40, 130])
+def test_qmm_dtypes_bits_groups(dtype, bits, gs, M):
+    r = rng(300 + M + bits)
+    K, N = 512, 200  # N not a multiple of 32: ragged output tiles
+    x = oracle.round_to(r.normal(0, 1, (M, K)), dtype)
+    wq, s, b = _quant(9 + bits, N, K, gs, bits, dtype)
+    y = ops.quantized_matmul(to_torch(x, dtype), *_dev(wq, s, b, dtype), group_size=gs, bits=bits)
+    want = oracle.quantized_matmul(x, wq, s, b, gs, bits, dtype)
+    tol = 2e-5 if dtype == "float32" else None
+    _close(y, want, dtype, tol)
+
+
+@pytest.mark.parametrize("M", [1, 64, 128])
+def test_qmm_special_cases(M):
+    """x = 0 -> 0 exactly; one-hot rows -> dequantized columns exactly."""
+    K, N = 1024, 96
+    wq, s, b = _quant(11, N, K)
+    W = oracle.dequantize(wq, s, b, 64, 4, "bfloat16")
+    dev = _dev(wq, s, b, "bfloat16")
+    zero = ops.quantized_matmul(torch.zeros((M, K), dtype=torch.bfloat16, device="cuda"), *dev)
+    assert bool((zero == 0).all())
+    x = np.zeros((M, K), np.float32)
+    ks = (np.arange(M) * 37) % K
+    x[np.arange(M), ks] = 1.0
+    y = to_np(ops.quantized_matmul(to_torch(x, "bfloat16"), *dev))
+    assert np.array_equal(y, W[:, ks].T)
+
+
+@pytest.mark.parametrize("M", [3, 70])
+def test_qmm_k_off_the_mfma_step_uses_generic_path(M):
+    """K = 160 at group 32: a valid MLX shape that is not a multiple of the
+    MFMA kernel's 64-value super-step, so every M runs the generic kernel."""
+    r = rng(12)
+    x = oracle.round_to(r.normal(0, 1, (M, 160)), "bfloat16")
+    wq, s, b = _quant(13, 64, 160, gs=32)
+    y = ops.quantized_matmul(to_torch(x, "bfloat16"), *_dev(wq, s, b, "bfloat16"), group_size=32)
+    _close(y, oracle.quantized_matmul(x, wq, s, b, 32, 4, "bfloat16"), "bfloat16")
+
+
+def test_qmm_rejects_bad_shapes():
+    wq, s, b = _quant(14, 32, 256)
+    dev = _dev(wq, s, b, "bfloat16")
+    with pytest.raises(ValueError):
+        ops.quantized_matmul(torch.zeros((2, 128), dtype=torch.bfloat16, device="cuda"), *dev)
+    with pytest.raises(ValueError):
+        ops.quantized_matmul(torch.zeros((2, 256), dtype=torch.bfloat16, device="cuda"), *dev, bits=3)
+
+
+# ---------------------------------------------------------- region epilogues
+
+
+@pytest.mark.parametrize("M", [1, 16, 128])
+def test_qmm_residual(M):
+    r = rng(400 + M)
+    K, N = 2048, 512
+    x = oracle.round_to(r.normal(0, 1, (1, M, K)), "bfloat16")
+    res = oracle.round_to(r.normal(0, 1, (1, M, N)), "bfloat16")
+    wq, s, b = _quant(15, N, K)
+    y = ops.qmm_residual(to_torch(x, "bfloat16"), *_dev(wq, s, b, "bfloat16"), to_torch(res, "bfloat16"))
+    t = oracle.quantized_matmul(x, wq, s, b, 64, 4, "bfloat16")
+    _close(y, oracle.round_to(res.astype(np.float64) + t, "bfloat16"), "bfloat16")
+
+
+@pytest.mark.parametrize("M", [1, 128])
+def test_qmm_residual_rmsnorm(M):
+    r = rng(500 + M)
+    K, N = 1024, 2048
+    x = oracle.round_to(r.normal(0, 1, (1, M, K)), "bfloat16")
+    res = oracle.round_to(r.normal(0, 1, (1, M, N)), "bfloat16")
+    nw = oracle.round_to(1 + 0.1 * r.normal(0, 1, N), "bfloat16")
+    wq, s, b = _quant(16, N, K)
+    h, y = ops.qmm_residual_rmsnorm(to_torch(x, "bfloat16"), *_dev(wq, s, b, "bfloat16"),
+                                    to_torch(res, "bfloat16"), to_torch(nw, "bfloat16"), 1e-5)
+    h_want = oracle.round_to(res.astype(np.float64) + oracle.quantized_matmul(x, wq, s, b, 64, 4, "bfloat16"), "bfloat16")
+    _close(h, h_want, "bfloat16")
+    # the norm stage is checked on the kernel's own h: bit-level agreement of the
+    # two-rounding form up to the rsqrt's last bit
+    _close(y, oracle.rms_norm(to_np(h), nw, 1e-5, "bfloat16"), "bfloat16")
+
+
+@pytest.mark.parametrize("M", [1, 100])
+def test_qmm_split_gate(M):
+    r = rng(600 + M)
+    K, D = 1024, 256
+    x = oracle.round_to(r.normal(0, 1, (1, M, K)), "bfloat16")
+    wq, s, b = _quant(17, 3 * D, K)
+    c, bx = ops.qmm_split_gate(to_torch(x, "bfloat16"), *_dev(wq, s, b, "bfloat16"))
+    full = oracle.quantized_matmul(x, wq, s, b, 64, 4, "bfloat16")
+    c_want, bx_want = oracle.split_gate(full, "bfloat16")
+    _close(c, c_want, "bfloat16")
+    _close(bx, bx_want, "bfloat16")
+
+
+@pytest.mark.parametrize("M", [1, 128])
+def test_qmm_dual_and_swiglu(M):
+    r = rng(700 + M)
+    K, N = 1024, 384
+    x = oracle.round_to(r.normal(0, 1, (1, M, K)), "bfloat16")
+    q1 = _quant(18, N, K)
+    q3 = _quant(19, N, K)
+    xd = to_torch(x, "bfloat16")
+    g, u = ops.qmm_dual(xd, *_dev(*q1, "bfloat16"), *_dev(*q3, "bfloat16"))
+    gw = oracle.quantized_matmul(x, *q1, 64, 4, "bfloat16")
+    uw = oracle.quantized_matmul(x, *q3, 64, 4, "bfloat16")
+    _close(g, gw, "bfloat16")
+    _close(u, uw, "bfloat16")
+    sw = ops.qmm_dual(xd, *_dev(*q1, "bfloat16"), *_dev(*q3, "bfloat16"), swiglu=True)
+    _close(sw, oracle.swiglu(gw, uw, "bfloat16"), "bfloat16")
+    # fused epilogue == swiglu of the unfused outputs, bit for bit
+    assert torch.equal(sw, ops.swiglu(g, u))
+
+
+# ------------------------------------------------------------------ A5-A10
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("D", [2560, 2048, 100])
+def test_rms_norm(dtype, D):
+    r = rng(800 + D)
+    x = oracle.round_to(r.normal(0, 1, (3, 37, D)), dtype)
+    w = oracle.round_to(1 + 0.2 * r.normal(0, 1, D), dtype)
+    y = ops.rms_norm(to_torch(x, dtype), to_torch(w, dtype), 1e-6)
+    _close(y, oracle.rms_norm(x, w, 1e-6, dtype), dtype, 1e-5 if dtype == "float32" else None)
+
+
+def test_rms_norm_eps_placement_gpu():
+    x = np.full((2, 32), 0.5, np.float32)
+    y = to_np(ops.rms_norm(to_torch(x, "float32"), to_torch(np.full(32, 1.5, np.float32), "float32"), 0.25))
+    assert y[0, 0] == pytest.approx(1.5 * 0.5 / math.sqrt(0.5), rel=1e-6)
+
+
+@pytest.mark.parametrize("H,D,L,offset,norm", [(32, 128, 128, 0, True), (8, 128, 1, 128, True),
+                                                (32, 64, 64, 5, True), (4, 128, 7, 0, False)])
+def test_norm_rope(H, D, L, offset, norm):
+    r = rng(900 + H + D + L)
+    x = oracle.round_to(r.normal(0, 1, (1, L, H * D)), "bfloat16")
+    w = oracle.round_to(1 + 0.2 * r.normal(0, 1, D), "bfloat16") if norm else None
+    got = ops.norm_rope(to_torch(x, "bfloat16"), None if w is None else to_torch(w, "bfloat16"),
+                        H, 1e-6, D, 1e6, offset)
+    want = oracle.norm_rope(x, w, 1e-6, H, D, 1e6, offset, "bfloat16")
+    _close(got, want, "bfloat16")
+
+
+def test_rope_partial_traditional_fp32():
+    r = rng(950)
+    x = r.normal(0, 1, (2, 3, 9, 32)).astype(np.float32)
+    for trad in (False, True):
+        got = ops.rope(to_torch(x, "float32"), 24, traditional=trad, base=1e4, offset=11)
+        _close(got, oracle.rope(x, 24, trad, 1e4, 1.0, 11, "float32"), "float32", 2e-5)
+
+
+def test_norm_rope_into_cache():
+    r = rng(960)
+    H, D, cap = 8, 128, 64
+    x = oracle.round_to(r.normal(0, 1, (1, 5, H * D)), "bfloat16")
+    cache = torch.full((1, H, cap, D), 7.0, dtype=torch.bfloat16, device="cuda")
+    ops.norm_rope(to_torch(x, "bfloat16"), None, H, 0.0, D, 1e6, 10, out=cache, out_pos=10)
+    want = oracle.norm_rope(x, None, 0.0, H, D, 1e6, 10, "bfloat16")
+    c = to_np(cache)
+    _close(c[:, :, 10:15], want, "bfloat16")
+    assert (c[:, :, :10] == 7.0).all() and (c[:, :, 15:] == 7.0).all()
+
+
+@pytest.mark.parametrize("H,HK,Lq,Lk,D,causal", [(32, 8, 128, 128, 128, True),
+                                                 (32, 8, 1, 129, 128, True),
+                                                 (32, 8, 200, 200, 64, True),
+                                                 (8, 8, 40, 70, 64, True),
+                                                 (6, 2, 33, 33, 128, False),
+                                                 (12, 4, 5, 130, 128, True)])
+def test_sdpa(H, HK, Lq, Lk, D, causal):
+    r = rng(1000 + Lq + Lk + D)
+    q = oracle.round_to(r.normal(0, 1, (1, H, Lq, D)), "bfloat16")
+    k = oracle.round_to(r.normal(0, 1, (1, HK, Lk, D)), "bfloat16")
+    v = oracle.round_to(r.normal(0, 1, (1, HK, Lk, D)), "bfloat16")
+    scale = D ** -0.5
+    want = oracle.sdpa(q, k, v, scale, causal, "bfloat16")
+    o = ops.scaled_dot_product_attention(to_torch(q, "bfloat16"), to_torch(k, "bfloat16"),
+                                         to_torch(v, "bfloat16"), scale, "causal" if causal else None)
+    _close(o, want, "bfloat16")
+    o1 = ops.scaled_dot_product_attention(to_torch(q, "bfloat16"), to_torch(k, "bfloat16"),
+                                          to_torch(v, "bfloat16"), scale,
+                                          "causal" if causal else None, out_layout=1)
+    assert torch.equal(o1, o.transpose(1, 2).contiguous())
+
+
+def test_sdpa_kv_cache_capacity():
+    """Only the first kv_len rows of a larger cache are read."""
+    r = rng(1100)
+    q = oracle.round_to(r.normal(0, 1, (1, 4, 3, 64)), "bfloat16")
+    k = oracle.round_to(r.normal(0, 1, (1, 2, 40, 64)), "bfloat16")
+    v = oracle.round_to(r.normal(0, 1, (1, 2, 40, 64)), "bfloat16")
+    kd, vd = to_torch(k, "bfloat16"), to_torch(v, "bfloat16")
+    kd[:, :, 20:] = float("nan")
+    vd[:, :, 20:] = float("nan")
+    o = ops.scaled_dot_product_attention(to_torch(q, "bfloat16"), kd, vd, 0.125, "causal", kv_len=20)
+    _close(o, oracle.sdpa(q, k[:, :, :20], v[:, :, :20], 0.125, True, "bfloat16"), "bfloat16")
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
+@pytest.mark.parametrize("n", [128 * 9728, 1001])
+def test_swiglu(dtype, n):
+    r = rng(1200)
+    g = oracle.round_to(r.normal(0, 2, n), dtype)
+    u = oracle.round_to(r.normal(0, 1, n), dtype)
+    y = ops.swiglu(to_torch(g, dtype), to_torch(u, dtype))
+    _close(y, oracle.swiglu(g, u, dtype), dtype, 1e-5 if dtype == "float32" else None)
+
+
+@pytest.mark.parametrize("L,with_state", [(2048, False), (1, True), (5, True)])
+def test_shortconv(L, with_state):
+    r = rng(1300 + L)
+    B, D = 1, 2048
+    bx = oracle.round_to(r.normal(0, 1, (B, L, D)), "bfloat16")
+    c = oracle.round_to(r.normal(0, 1, (B, L, D)), "bfloat16")
+    w = oracle.round_to(r.normal(0, 0.5, (D, 3)), "bfloat16")
+    st = oracle.round_to(r.normal(0, 1, (B, 2, D)), "bfloat16") if with_state else None
+    out, st_out = ops.shortconv(to_torch(bx, "bfloat16"), to_torch(c, "bfloat16"),
+                                to_torch(w, "bfloat16"), None if st is None else to_torch(st, "bfloat16"))
+    want, st_want = oracle.shortconv(bx, c, w, st, "bfloat16")
+    _close(out, want, "bfloat16")
+    assert np.array_equal(to_np(st_out), st_want)
+
+
+def test_linear_gelu_f32():
+    r = rng(1400)
+    x = r.normal(0, 1, (32, 256)).astype(np.float32)
+    w1 = r.normal(0, 0.02, (1024, 256)).astype(np.float32)
+    b1 = r.normal(0, 0.1, 1024).astype(np.float32)
+    h = ops.linear_f32(to_torch(x, "float32"), to_torch(w1, "float32"), to_torch(b1, "float32"), gelu=True)
+    want = oracle.gelu(x.astype(np.float64) @ w1.T.astype(np.float64) + b1).astype(np.float32)
+    _close(h, want, "float32", 1e-5)
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+def test_argmax_lowest_index_on_ties(dtype):
+    r = rng(1500)
+    x = oracle.round_to(r.normal(0, 1, (3, 151936)), dtype)
+    x[1, 77] = x[1, 90000] = 50.0          # tie: lowest index wins
+    x[2, :] = -1.0
+    x[2, 5] = float("nan")                  # NaN never wins
+    got = ops.argmax(to_torch(x, dtype)).cpu().numpy()
+    assert got[0] == int(np.argmax(x[0]))
+    assert got[1] == 77
+    assert got[2] == 0
+
+
+def test_determinism_three_runs():
+    """The reference's gate: three runs bitwise identical (ladder/child.py:419-428)."""
+    r = rng(1600)
+    x = to_torch(oracle.round_to(r.normal(0, 1, (128, 2560)), "bfloat16"), "bfloat16")
+    dev = _dev(*_quant(20, 9728, 2560), "bfloat16")
+    outs = [ops.quantized_matmul(x, *dev) for _ in range(3)]
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
