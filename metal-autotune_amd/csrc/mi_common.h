@@ -83,7 +83,23 @@ __device__ __forceinline__ typename Vec<T>::x8 dequant8(uint32_t w0, uint32_t w1
     return r;
 }
 
+// Register "launder": an empty asm that claims to rewrite the value. Placed
+// where a prefetched register buffer is handed to the next pipeline step, it
+// stops the compiler from folding the two loads feeding that hand-off into one
+// load at the top of the loop (which would serialize load and use); the wait
+// for the prefetched data then lands at the hand-off, after the compute.
+__device__ __forceinline__ void launder(uint4 &v) {
+    asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+}
+__device__ __forceinline__ void launder(uint32_t &v) { asm volatile("" : "+v"(v)); }
+
 __host__ __device__ constexpr int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline int ilog2(int v) {
+    int r = 0;
+    while ((1 << (r + 1)) <= v) ++r;
+    return r;
+}
 
 inline hipStream_t as_stream(void *s) { return (hipStream_t)s; }
 

@@ -45,6 +45,7 @@ struct QParams {
     void *y1;                  // T [M, Nout] (EPI_SPLIT3, EPI_DUAL)
     int64_t M, Nout, K;
     int gs;
+    int gs_log2;               // log2(gs): group sizes are powers of two
     int wk;                    // K-split waves (qmm_mfma_kernel)
 };
 
@@ -168,48 +169,207 @@ __global__ __launch_bounds__(256) void qmv_kernel(QParams p) {
 #pragma unroll
         for (int m = 0; m < MR; ++m) acc[q][m] = 0.0f;
 
-    if (n < p.Nout) {
-        const uint32_t *wr[P];
-        const T *sr[P];
-        const T *br[P];
+    // out-of-range rows/tokens read clamped, valid addresses (no branch around
+    // loads); their sums are never stored
+    const int64_t nrow = n < p.Nout ? n : p.Nout - 1;
+    const uint32_t *wr[P];
+    const T *sr[P];
+    const T *br[P];
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+        const int64_t row = p.noff[q] + nrow;
+        wr[q] = p.w[q] + row * (K / VPW);
+        sr[q] = (const T *)p.s[q] + row * G;
+        br[q] = (const T *)p.b[q] + row * G;
+    }
+#pragma unroll 2
+    for (int64_t c = j; c < cpr; c += 16) {
+        const int64_t k0 = c * VPC;
+        float qf[P][VPC];
+        float sc[P], bi[P];
 #pragma unroll
         for (int q = 0; q < P; ++q) {
-            const int64_t row = p.noff[q] + n;
-            wr[q] = p.w[q] + row * (K / VPW);
-            sr[q] = (const T *)p.s[q] + row * G;
-            br[q] = (const T *)p.b[q] + row * G;
+            const uint4 wv = ld16(wr[q] + c * 4);
+            const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+            for (int i = 0; i < VPC; ++i)
+                qf[q][i] =
+                    (float)((words[i / VPW] >> ((i % VPW) * BITS)) & ((1u << BITS) - 1u));
+            sc[q] = (float)sr[q][k0 >> p.gs_log2];
+            bi[q] = (float)br[q][k0 >> p.gs_log2];
         }
-#pragma unroll 2
-        for (int64_t c = j; c < cpr; c += 16) {
-            const int64_t k0 = c * VPC;
-            float qf[P][VPC];
-            float sc[P], bi[P];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            float xf[VPC];
+            load_x<T, VPC>(x + (m < mr ? m : mr - 1) * K + k0, xf);
+            float dx = 0.0f;
+#pragma unroll
+            for (int i = 0; i < VPC; ++i) dx += xf[i];
 #pragma unroll
             for (int q = 0; q < P; ++q) {
-                const uint4 wv = ld16(wr[q] + c * 4);
-                const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+                float dq = 0.0f;
 #pragma unroll
-                for (int i = 0; i < VPC; ++i)
-                    qf[q][i] = (float)((words[i / VPW] >> ((i % VPW) * BITS)) &
-                                       ((1u << BITS) - 1u));
-                sc[q] = (float)sr[q][k0 / p.gs];
-                bi[q] = (float)br[q][k0 / p.gs];
+                for (int i = 0; i < VPC; ++i) dq = __builtin_fmaf(xf[i], qf[q][i], dq);
+                acc[q][m] += sc[q] * dq + bi[q] * dx;
             }
+        }
+    }
 #pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                if (m < mr) {
-                    float xf[VPC];
-                    load_x<T, VPC>(x + m * K + k0, xf);
-                    float dx = 0.0f;
+    for (int q = 0; q < P; ++q)
 #pragma unroll
-                    for (int i = 0; i < VPC; ++i) dx += xf[i];
+        for (int m = 0; m < MR; ++m) {
+            float v = acc[q][m];
+            v += __shfl_xor(v, 8, 16);
+            v += __shfl_xor(v, 4, 16);
+            v += __shfl_xor(v, 2, 16);
+            v += __shfl_xor(v, 1, 16);
+            acc[q][m] = v;
+        }
+    if (j == 0 && n < p.Nout) {
 #pragma unroll
-                    for (int q = 0; q < P; ++q) {
-                        float dq = 0.0f;
+        for (int m = 0; m < MR; ++m) {
+            if (m < mr) {
+                float a[P];
 #pragma unroll
-                        for (int i = 0; i < VPC; ++i) dq = __builtin_fmaf(xf[i], qf[q][i], dq);
-                        acc[q][m] += sc[q] * dq + bi[q] * dx;
+                for (int q = 0; q < P; ++q) a[q] = acc[q][m];
+                epi1<T, EPI>(p, m0 + m, n, a);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Decode GEMV (M <= 4, 4-bit, bf16/fp16): the nibbles never go through a
+// float conversion. (w >> 4j) & 0x000F000F | MAGIC packs nibbles j and j+4 of a
+// word as the two 16-bit floats MAG + q exactly (bf16: 0x4300 = 128, ulp 1 up
+// to 256; fp16: 0x6400 = 1024, ulp 1), so one v_and_or makes a pair and
+// v_dot2_f32_{bf16,f16} multiplies it with the x pair (x[k], x[k+4]):
+//   sum_k x_k (MAG + q_k) = D  ->  s*sum(x q) + b*sum(x) = s*D + (b - MAG*s)*sum(x).
+// x is staged once per workgroup in LDS already permuted into those pairs,
+// with per-32-value chunk sums. Weight chunks are loaded 8 per lane before use.
+
+template <typename T> struct Magic;
+template <> struct Magic<bf16> {
+    static constexpr uint32_t pair = 0x43004300u;
+    static constexpr float value = 128.0f;
+    static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+        typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b),
+                                               c, false);
+    }
+};
+template <> struct Magic<f16> {
+    static constexpr uint32_t pair = 0x64006400u;
+    static constexpr float value = 1024.0f;
+    static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+        typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c,
+                                      false);
+    }
+};
+
+constexpr int QV_BATCH = 8;  // 16-byte weight chunks in flight per lane
+
+inline int64_t qmv_dot2_lds_bytes(int mr, int64_t K) { return mr * K * 2 + mr * (K / 32) * 4; }
+
+template <typename T, int MR, int EPI>
+__global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
+    constexpr int P = epi_parts(EPI);
+    typedef Magic<T> Mg;
+    extern __shared__ uint4 xs_pairs[];  // [MR][K/8] pair blocks, then [MR][K/32] sums
+    const int64_t K = p.K, words = K / 8, cpr = K / 32, G = K / p.gs;
+    float *xsum = (float *)(xs_pairs + MR * words);
+    const int lane = threadIdx.x & 63, j = lane & 15;
+    const int64_t n = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 6) * 4 + (lane >> 4);
+    const int64_t nrow = n < p.Nout ? n : p.Nout - 1;
+    const int64_t m0 = (int64_t)blockIdx.y * MR;
+    const int mr = (int)((p.M - m0) < MR ? (p.M - m0) : MR);
+
+    const uint32_t *wr[P];
+    const T *sr[P];
+    const T *br[P];
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+        const int64_t row = p.noff[q] + nrow;
+        wr[q] = p.w[q] + row * (K / 8);
+        sr[q] = (const T *)p.s[q] + row * G;
+        br[q] = (const T *)p.b[q] + row * G;
+    }
+
+    // stage x rows as pairs (e[i], e[i+4]) of each 8-value block
+    const T *x = (const T *)p.x + m0 * K;
+    for (int64_t idx = threadIdx.x; idx < MR * words; idx += 256) {
+        const int64_t m = idx / words, w = idx - m * words;
+        const uint4 d = ld16(x + (m < mr ? m : mr - 1) * K + 8 * w);
+        xs_pairs[idx] = make_uint4(__builtin_amdgcn_perm(d.z, d.x, 0x05040100u),
+                                   __builtin_amdgcn_perm(d.z, d.x, 0x07060302u),
+                                   __builtin_amdgcn_perm(d.w, d.y, 0x05040100u),
+                                   __builtin_amdgcn_perm(d.w, d.y, 0x07060302u));
+    }
+    __syncthreads();
+    for (int64_t idx = threadIdx.x; idx < MR * cpr; idx += 256) {
+        const int64_t m = idx / cpr, c = idx - m * cpr;
+        float s = 0.0f;
+#pragma unroll
+        for (int wi = 0; wi < 4; ++wi) {
+            const uint4 v = xs_pairs[m * words + 4 * c + wi];
+            float f[8];
+            unpack8<T>(v, f);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s += f[i];
+        }
+        xsum[idx] = s;
+    }
+    __syncthreads();
+
+    float acc[P][MR];
+#pragma unroll
+    for (int q = 0; q < P; ++q)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[q][m] = 0.0f;
+
+    for (int64_t base = j; base < cpr; base += 16 * QV_BATCH) {
+        uint4 wv[P][QV_BATCH];
+        T sv[P][QV_BATCH], bv[P][QV_BATCH];
+#pragma unroll
+        for (int i = 0; i < QV_BATCH; ++i) {
+            const int64_t c = base + 16 * i;
+            const int64_t cc = c < cpr ? c : cpr - 1;
+            const int64_t g = (cc * 32) >> p.gs_log2;
+#pragma unroll
+            for (int q = 0; q < P; ++q) {
+                wv[q][i] = ld16(wr[q] + 4 * cc);
+                sv[q][i] = sr[q][g];
+                bv[q][i] = br[q][g];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < QV_BATCH; ++i) {
+            const int64_t c = base + 16 * i;
+            if (c >= cpr) break;
+#pragma unroll
+            for (int q = 0; q < P; ++q) {
+                const uint32_t wd[4] = {wv[q][i].x, wv[q][i].y, wv[q][i].z, wv[q][i].w};
+                uint32_t qp[4][4];
+#pragma unroll
+                for (int wi = 0; wi < 4; ++wi)
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj)
+                        qp[wi][jj] = ((wd[wi] >> (4 * jj)) & 0x000F000Fu) | Mg::pair;
+                const float s = (float)sv[q][i];
+                const float bb = __builtin_fmaf(-Mg::value, s, (float)bv[q][i]);
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    float d = 0.0f;
+#pragma unroll
+                    for (int wi = 0; wi < 4; ++wi) {
+                        const uint4 xp = xs_pairs[m * words + 4 * c + wi];
+                        d = Mg::dot2(qp[wi][0], xp.x, d);
+                        d = Mg::dot2(qp[wi][1], xp.y, d);
+                        d = Mg::dot2(qp[wi][2], xp.z, d);
+                        d = Mg::dot2(qp[wi][3], xp.w, d);
                     }
+                    acc[q][m] += s * d + bb * xsum[m * cpr + c];
                 }
             }
         }
@@ -254,52 +414,103 @@ template <> struct Mfma<f16> {
 };
 
 // A: 32-row weight tiles per wave (one per part when P > 1); C: 32-token
-// tiles per wave; WN: waves along N; WKMAX: the largest K split (p.wk <= it).
-template <typename T, int BITS, int A, int C, int WN, int WKMAX, int EPI>
-__global__ __launch_bounds__(64 * WN * WKMAX) void qmm_mfma_kernel(QParams p) {
+// tiles per wave; WK: waves per workgroup, each owning a 1/wk slice of K.
+//
+// x reaches the MFMAs through LDS: each wave streams its own K slice of the
+// token tile into its own double-buffered LDS region with direct-to-LDS DMA
+// (global_load_lds_dwordx4), 8 rows x 128 bytes per instruction, so every x
+// cache line is fetched once. (Loading x fragments straight into registers
+// makes each lane read a different token row; with four waves the per-step
+// working set overflows the 32 KB L1 and every 16-byte use re-fetches a line.)
+// The 16-byte chunks of a row are XOR-swizzled by (row >> 1) & 7 so a
+// 16-lane ds_read_b128 group covers 16 distinct bank groups. Weight fragments
+// go straight to registers (each element is used by exactly one lane).
+constexpr int XK = 64;  // k values per x stage (128 bytes of a token row)
+
+template <typename T, int BITS, int A, int C, int WK>
+struct MfmaShape {
+    static constexpr int VPW = 32 / BITS;  // values per word
+    static constexpr int VPC = 4 * VPW;    // values per 16-byte weight chunk (per lane half)
+    static constexpr int S = VPC / 8;      // MFMA steps per super-step
+    static constexpr int SS = 2 * VPC;     // k per super-step
+    static constexpr int SPS = XK / SS;    // super-steps per x stage
+    static constexpr int ROWS = 32 * C;    // token rows per stage
+    static constexpr int STAGE = ROWS * 128;                          // bytes per x stage
+    static constexpr int XBYTES = WK * 2 * STAGE;                     // x staging
+    static constexpr int RBYTES = (WK - 1) * A * C * 16 * 64 * 4;     // K-split reduction
+    static constexpr int LDS = XBYTES > RBYTES ? XBYTES : RBYTES;
+};
+
+template <typename T, int BITS, int A, int C, int WK, int EPI>
+__global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
+    typedef MfmaShape<T, BITS, A, C, WK> Sh;
     constexpr int P = epi_parts(EPI);
     static_assert(P == 1 || A == P, "multi-part epilogues use one tile per part");
     constexpr int TN = (P == 1) ? A : 1;  // 32-wide output tiles per wave
-    constexpr int VPW = 32 / BITS;        // values per word
-    constexpr int VPC = 4 * VPW;          // values per 16-byte chunk (per lane half)
-    constexpr int S = VPC / 8;            // MFMA steps per super-step
-    constexpr int SS = 2 * VPC;           // k per super-step
+    constexpr int VPW = Sh::VPW, VPC = Sh::VPC, S = Sh::S, SS = Sh::SS, SPS = Sh::SPS;
     typedef typename Vec<T>::x8 V8;
+    __shared__ __attribute__((aligned(16))) char lds[Sh::LDS];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int wn = wave % WN, kw = wave / WN;
+    const int kw = threadIdx.x >> 6;
     const int h = lane >> 5, r = lane & 31;
     const int64_t K = p.K, G = K / p.gs;
-    const int64_t n_wave = (int64_t)blockIdx.x * (32 * TN * WN) + wn * 32 * TN;
+    const int64_t n_wave = (int64_t)blockIdx.x * (32 * TN);
     const int64_t m_blk = (int64_t)blockIdx.y * (32 * C);
     const int wk = p.wk;
-    const int64_t Kw = K / wk;
-    const int64_t kbeg = kw * Kw;
-    const int nsteps = (int)(Kw / SS);
+    const int Kw = (int)(K / wk);
+    const int kbeg = kw * Kw;
+    const int nst = Kw / XK;
+    char *xbuf = lds + kw * 2 * Sh::STAGE;
 
+    // Rows past N (or tokens past M) read a clamped, valid row instead of
+    // branching around the load: their accumulators only feed outputs the
+    // epilogue never stores, and branch-free loads keep the prefetch in flight.
     const uint32_t *wrow[A];
-    const T *srow[A];
-    const T *brow[A];
-    bool wok[A];
+    const uint16_t *srow[A], *brow[A];
 #pragma unroll
     for (int a = 0; a < A; ++a) {
         const int part = (P == 1) ? 0 : a;
         const int64_t nout = n_wave + ((P == 1) ? 32 * a : 0) + r;
-        wok[a] = nout < p.Nout;
-        const int64_t row = p.noff[part] + (wok[a] ? nout : 0);
+        const int64_t row = p.noff[part] + (nout < p.Nout ? nout : p.Nout - 1);
         wrow[a] = p.w[part] + row * (K / VPW) + 4 * h;
-        srow[a] = (const T *)p.s[part] + row * G;
-        brow[a] = (const T *)p.b[part] + row * G;
+        srow[a] = (const uint16_t *)p.s[part] + row * G;
+        brow[a] = (const uint16_t *)p.b[part] + row * G;
     }
-    const T *xrow[C];
-    bool xok[C];
+    // x DMA: instruction i writes stage rows 8i..8i+7; lane l fills row
+    // 8i + l/8 at swizzled position l%8, i.e. it loads chunk (l%8) ^ swz(row).
+    const T *xbase = (const T *)p.x + kbeg;
+    int xoff[C * 4];
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-        const int64_t m = m_blk + 32 * c + r;
-        xok[c] = m < p.M;
-        xrow[c] = (const T *)p.x + (xok[c] ? m : 0) * K + h * VPC;
+    for (int i = 0; i < C * 4; ++i) {
+        const int row = 8 * i + (lane >> 3);
+        const int64_t m = m_blk + row < p.M ? m_blk + row : p.M - 1;
+        const int chunk = (lane & 7) ^ ((row >> 1) & 7);
+        xoff[i] = (int)(m * K) + 8 * chunk;
     }
+    auto issue_x = [&](int st, int buf) {
+        char *dst = xbuf + buf * Sh::STAGE;
+#pragma unroll
+        for (int i = 0; i < C * 4; ++i)
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void *)(xbase + xoff[i] + st * XK),
+                (__attribute__((address_space(3))) void *)(dst + i * 1024), 16, 0, 0);
+    };
+    const int gshift = p.gs_log2;
+    auto issue_w = [&](int st, uint4 (&wd)[A][SPS], uint32_t (&sd)[A][SPS],
+                       uint32_t (&bd)[A][SPS]) {
+#pragma unroll
+        for (int u = 0; u < SPS; ++u) {
+            const int k0 = kbeg + st * XK + u * SS;
+            const int g = (k0 + h * VPC) >> gshift;
+#pragma unroll
+            for (int a = 0; a < A; ++a) {
+                wd[a][u] = ld16(wrow[a] + k0 / VPW);
+                sd[a][u] = srow[a][g];
+                bd[a][u] = brow[a][g];
+            }
+        }
+    };
 
     f32x16 acc[A][C];
 #pragma unroll
@@ -309,62 +520,73 @@ __global__ __launch_bounds__(64 * WN * WKMAX) void qmm_mfma_kernel(QParams p) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[a][c][i] = 0.0f;
 
-    // software pipeline: fragments of step t+1 load while step t computes
-    uint4 wv[A], wn_[A];
-    float sv[A], bv[A], sn[A], bn[A];
-    uint4 xv[C][S], xn[C][S];
-    auto load = [&](int64_t k0, uint4 (&wd)[A], float (&sd)[A], float (&bd)[A],
-                    uint4 (&xd)[C][S]) {
-#pragma unroll
-        for (int a = 0; a < A; ++a) {
-            wd[a] = wok[a] ? ld16(wrow[a] + k0 / VPW) : make_uint4(0, 0, 0, 0);
-            const int64_t g = (k0 + h * VPC) / p.gs;
-            sd[a] = wok[a] ? (float)srow[a][g] : 0.0f;
-            bd[a] = wok[a] ? (float)brow[a][g] : 0.0f;
-        }
+    // Pipeline: at the top of stage st every load issued during stage st-1
+    // (x DMA into buffer st&1, weights into wn_) has landed; the stage's x
+    // fragments are read out of LDS first, then the loads of stage st+1 are
+    // issued and overlap this stage's MFMAs.
+    uint4 wv[A][SPS], wn_[A][SPS];
+    uint32_t sv[A][SPS], bv[A][SPS], sn[A][SPS], bn[A][SPS];
+    if (nst > 0) {
+        issue_x(0, 0);
+        issue_w(0, wv, sv, bv);
+    }
+    const int swz = (r >> 1) & 7;
+    for (int st = 0; st < nst; ++st) {
+        const char *cur = xbuf + (st & 1) * Sh::STAGE;
+        // vmcnt(0): the x DMA and weight loads issued during stage st-1
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        uint4 xf[C][SPS][S];
 #pragma unroll
         for (int c = 0; c < C; ++c)
 #pragma unroll
+            for (int u = 0; u < SPS; ++u)
+#pragma unroll
+                for (int j = 0; j < S; ++j) {
+                    const int chunk = (u * SS + h * VPC + 8 * j) >> 3;
+                    xf[c][u][j] = *(const uint4 *)(cur + (32 * c + r) * 128 + ((chunk ^ swz) << 4));
+                }
+        const int nx = (st + 1 < nst) ? st + 1 : st;
+        if (st + 1 < nst) issue_x(nx, (st + 1) & 1);  // wave-uniform branch
+        issue_w(nx, wn_, sn, bn);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < SPS; ++u)
+#pragma unroll
             for (int j = 0; j < S; ++j)
-                xd[c][j] = xok[c] ? ld16(xrow[c] + k0 + 8 * j) : make_uint4(0, 0, 0, 0);
-    };
-    if (nsteps > 0) load(kbeg, wv, sv, bv, xv);
-    for (int t = 0; t < nsteps; ++t) {
-        if (t + 1 < nsteps) load(kbeg + (int64_t)(t + 1) * SS, wn_, sn, bn, xn);
 #pragma unroll
-        for (int j = 0; j < S; ++j) {
+                for (int a = 0; a < A; ++a) {
+                    const uint32_t words[4] = {wv[a][u].x, wv[a][u].y, wv[a][u].z, wv[a][u].w};
+                    const float sf = (float)__builtin_bit_cast(T, (uint16_t)sv[a][u]);
+                    const float bf = (float)__builtin_bit_cast(T, (uint16_t)bv[a][u]);
+                    const V8 af = (BITS == 4) ? dequant8<T, 4>(words[j], 0u, sf, bf)
+                                              : dequant8<T, 8>(words[2 * j], words[2 * j + 1], sf, bf);
 #pragma unroll
-            for (int a = 0; a < A; ++a) {
-                const uint32_t words[4] = {wv[a].x, wv[a].y, wv[a].z, wv[a].w};
-                const V8 af = (BITS == 4)
-                                  ? dequant8<T, 4>(words[j], 0u, sv[a], bv[a])
-                                  : dequant8<T, 8>(words[2 * j], words[2 * j + 1], sv[a], bv[a]);
+                    for (int c = 0; c < C; ++c)
+                        acc[a][c] = Mfma<T>::mma(af, __builtin_bit_cast(V8, xf[c][u][j]), acc[a][c]);
+                }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int c = 0; c < C; ++c)
-                    acc[a][c] = Mfma<T>::mma(af, __builtin_bit_cast(V8, xv[c][j]), acc[a][c]);
+        for (int a = 0; a < A; ++a)
+#pragma unroll
+            for (int u = 0; u < SPS; ++u) {
+                wv[a][u] = wn_[a][u];
+                sv[a][u] = sn[a][u];
+                bv[a][u] = bn[a][u];
+                launder(wv[a][u]);
+                launder(sv[a][u]);
+                launder(bv[a][u]);
             }
-        }
-        if (t + 1 < nsteps) {
-#pragma unroll
-            for (int a = 0; a < A; ++a) {
-                wv[a] = wn_[a];
-                sv[a] = sn[a];
-                bv[a] = bn[a];
-            }
-#pragma unroll
-            for (int c = 0; c < C; ++c)
-#pragma unroll
-                for (int j = 0; j < S; ++j) xv[c][j] = xn[c][j];
-        }
     }
 
-    if constexpr (WKMAX > 1) {
-        // fixed-order reduction of the K-split partial tiles through LDS
+    if constexpr (WK > 1) {
+        // fixed-order reduction of the K-split partial tiles; the LDS staging
+        // is reused, so every wave must be done with its x stages first
         constexpr int REGS = A * C * 16;
-        __shared__ float red[(WKMAX - 1) * WN * REGS * 64];
+        float *red = (float *)lds;
+        __syncthreads();
         if (wk > 1) {
             if (kw > 0) {
-                float *dst = red + ((size_t)((kw - 1) * WN + wn) * REGS) * 64 + lane;
+                float *dst = red + (size_t)(kw - 1) * REGS * 64 + lane;
 #pragma unroll
                 for (int a = 0; a < A; ++a)
 #pragma unroll
@@ -375,13 +597,13 @@ __global__ __launch_bounds__(64 * WN * WKMAX) void qmm_mfma_kernel(QParams p) {
             __syncthreads();
             if (kw > 0) return;
             for (int src = 1; src < wk; ++src) {
-                const float *s = red + ((size_t)((src - 1) * WN + wn) * REGS) * 64 + lane;
+                const float *sp = red + (size_t)(src - 1) * REGS * 64 + lane;
 #pragma unroll
                 for (int a = 0; a < A; ++a)
 #pragma unroll
                     for (int c = 0; c < C; ++c)
 #pragma unroll
-                        for (int i = 0; i < 16; ++i) acc[a][c][i] += s[((a * C + c) * 16 + i) * 64];
+                        for (int i = 0; i < 16; ++i) acc[a][c][i] += sp[((a * C + c) * 16 + i) * 64];
             }
         }
     }
@@ -432,34 +654,49 @@ int launch_qmv(const QParams &p, hipStream_t st) {
     return launch_status("quantized matmul (qmv)");
 }
 
-template <typename T, int BITS, int A, int C, int WN, int WKMAX, int EPI>
+template <typename T, int BITS, int A, int C, int EPI>
 int launch_mfma_cfg(QParams p, int wk, hipStream_t st) {
     constexpr int P = epi_parts(EPI);
     constexpr int TN = (P == 1) ? A : 1;
     p.wk = wk;
-    const dim3 grid((unsigned)ceil_div(p.Nout, 32 * TN * WN), (unsigned)ceil_div(p.M, 32 * C));
-    qmm_mfma_kernel<T, BITS, A, C, WN, WKMAX, EPI><<<grid, 64 * WN * wk, 0, st>>>(p);
+    const dim3 grid((unsigned)ceil_div(p.Nout, 32 * TN), (unsigned)ceil_div(p.M, 32 * C));
+    qmm_mfma_kernel<T, BITS, A, C, 4, EPI><<<grid, 64 * wk, 0, st>>>(p);
     return launch_status("quantized matmul (mfma)");
 }
 
+// K must split into wk slices of whole 64-value x stages.
 template <typename T, int BITS, int EPI>
 int launch_mfma(const QParams &p, hipStream_t st) {
     constexpr int P = epi_parts(EPI);
     constexpr int A = (P == 1) ? 2 : P;
-    constexpr int SS = 2 * 4 * (32 / BITS);
-    const int64_t ks = p.K / SS;  // super-steps
-    const int wk = (ks % 4 == 0) ? 4 : (ks % 2 == 0 ? 2 : 1);
-    if (p.M > 256) return launch_mfma_cfg<T, BITS, A, 4, 4, 1, EPI>(p, 1, st);
-    if (p.M > 64) return launch_mfma_cfg<T, BITS, A, 4, 1, 4, EPI>(p, wk, st);
-    if (p.M > 32) return launch_mfma_cfg<T, BITS, A, 2, 1, 4, EPI>(p, wk, st);
-    return launch_mfma_cfg<T, BITS, A, 1, 1, 4, EPI>(p, wk, st);
+    const int64_t stages = p.K / XK;
+    const int wk = (stages % 4 == 0) ? 4 : (stages % 2 == 0 ? 2 : 1);
+    if (p.M > 64) return launch_mfma_cfg<T, BITS, A, 4, EPI>(p, wk, st);
+    if (p.M > 32) return launch_mfma_cfg<T, BITS, A, 2, EPI>(p, wk, st);
+    return launch_mfma_cfg<T, BITS, A, 1, EPI>(p, wk, st);
+}
+
+template <typename T, int EPI>
+int launch_qmv_dot2(const QParams &p, int mr, hipStream_t st) {
+    const dim3 grid((unsigned)ceil_div(p.Nout, 16), (unsigned)ceil_div(p.M, mr));
+    const size_t lds = (size_t)qmv_dot2_lds_bytes(mr, p.K);
+    if (mr == 1)
+        qmv_dot2_kernel<T, 1, EPI><<<grid, 256, lds, st>>>(p);
+    else if (mr == 2)
+        qmv_dot2_kernel<T, 2, EPI><<<grid, 256, lds, st>>>(p);
+    else
+        qmv_dot2_kernel<T, 4, EPI><<<grid, 256, lds, st>>>(p);
+    return launch_status("quantized matmul (dot2 qmv)");
 }
 
 template <typename T, int EPI>
 int launch_typed(const QParams &p, int bits, hipStream_t st) {
-    const int SS = 2 * 4 * (32 / bits);
-    const bool mfma = (sizeof(T) == 2) && p.M > QMV_MR && (p.K % SS == 0);
+    const bool mfma = (sizeof(T) == 2) && p.M > QMV_MR && (p.K % XK == 0) &&
+                      p.M * p.K < ((int64_t)1 << 31);
     if constexpr (sizeof(T) == 2) {
+        const int mr = p.M == 1 ? 1 : (p.M == 2 ? 2 : 4);
+        if (bits == 4 && p.M <= 4 && qmv_dot2_lds_bytes(mr, p.K) <= 65536)
+            return launch_qmv_dot2<T, EPI>(p, mr, st);
         if (mfma)
             return bits == 4 ? launch_mfma<T, 4, EPI>(p, st) : launch_mfma<T, 8, EPI>(p, st);
     }
@@ -492,6 +729,7 @@ QParams base_params(const void *x, const uint32_t *w, const void *s, const void 
     p.Nout = Nout;
     p.K = K;
     p.gs = gs;
+    p.gs_log2 = ilog2(gs);
     p.wk = 1;
     return p;
 }
