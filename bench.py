@@ -1,0 +1,261 @@
+"""Benchmark: Qwen3-4B-shaped 4-bit prefill of 128 tokens on one MI355X.
+
+`python bench.py [--gpus 1] [--steps K] [--warmup W]` prints ONE JSON line.
+
+A step is one prefill forward of BASELINE config 4's model (36 decoder layers,
+hidden 2560, 32/8 heads of 128, SwiGLU 9728, tied quantized embedding/lm_head
+V = 151936, every projection 4-bit affine group 64; random seeded weights and
+token ids) over 128 tokens: embedding gather, 36 layers with the region cuts
+installed, final norm and the lm_head for the last position, then the greedy
+token. The step is captured once into a HIP graph and replayed (no host work
+in the timed region); inputs are resident in HBM.
+
+Also measured live, with HIP events on the stream the kernels run on:
+  - roofline: the dominant kernel (the M=128 gate/up qmm region of the model,
+    the largest GEMM) -- algorithmic flops per launch / average duration,
+    against MI355X's dense bf16 MFMA peak (2.5 PFLOP/s);
+  - qmm: BASELINE config 2 (x[M, 2560] @ W[9728, 2560]^T, 4-bit g64) at M=1
+    (HBM GB/s vs 8 TB/s) and M=128 (TFLOP/s vs the MFMA peak), rotating more
+    weight copies than the 256 MB Infinity Cache holds;
+  - cpu_baseline: the CPU oracle (the port; MLX is not installed) on a bounded
+    sample -- one decoder layer at L=128 plus the lm_head for one token --
+    scaled to the 36-layer model.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "metal-autotune_amd"))
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFS = 2500.0
+PROMPT = 128
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def graph_of(fn, torch):
+    """Capture fn() into a HIP graph on a side stream; returns (graph, output)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # eager run: allocations and library loading happen outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fn()
+    torch.cuda.synchronize()
+    return g, out
+
+
+def time_graph(g, reps, torch):
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) / reps  # ms
+
+
+def kernel_us(make_call, n_calls, torch, reps=5):
+    """Average duration of one call: n_calls launches captured in a graph, timed
+    with events on the capture stream's successor (the current stream)."""
+    def body():
+        for i in range(n_calls):
+            make_call(i)
+    g, _ = graph_of(body, torch)
+    g.replay()
+    torch.cuda.synchronize()
+    return time_graph(g, reps, torch) * 1000.0 / n_calls
+
+
+def qmm_config2(torch, ops):
+    """Config 2: x[M, 2560] bf16 @ W[9728, 2560]^T, 4-bit g64, M in {1, 128}."""
+    from workloads.quantize import random_quantized
+
+    N, K, gs = 9728, 2560, 64
+    wbytes = N * K // 2 + 2 * (N * K // gs) * 2
+    copies = (512 << 20) // wbytes + 1  # > 256 MB Infinity Cache
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    ws = [random_quantized(N, K, gen, "cuda") for _ in range(copies)]
+    out = {}
+    for M in (1, 16, 128):
+        x = torch.randn((M, K), generator=gen, device="cuda").to(torch.bfloat16)
+        y = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
+        from autotuner_runtime import hip
+        us = kernel_us(lambda i: hip.b_qmm([x, *ws[i % copies]], [y], {"group_size": gs, "bits": 4}),
+                       4 * copies, torch)
+        byts = wbytes + 2 * M * K + 2 * M * N
+        fl = 2 * M * N * K
+        out[f"M{M}"] = {"us": round(us, 2), "GB_s": round(byts / us / 1e3, 1),
+                        "hbm_frac": round(byts / us / 1e3 / HBM_PEAK_GBS, 4),
+                        "TFLOP_s": round(fl / us / 1e6, 2),
+                        "mfma_frac": round(fl / us / 1e6 / BF16_PEAK_TFS, 4),
+                        "bytes": byts, "flops": fl}
+    del ws
+    return out
+
+
+def dominant_kernel(model, torch, ops):
+    """The gate/up region (dual qmm + swiglu epilogue) at M=128 over the 36
+    layers' weights: 2 x 128 x 9728 x 2560 x 2 flops per launch."""
+    layers = [l.wrapped if hasattr(l, "wrapped") else l for l in model.model.layers]
+    x = torch.randn((1, PROMPT, model.cfg.hidden_size), device="cuda").to(torch.bfloat16)
+
+    def call(i):
+        m = layers[i % len(layers)].mlp
+        g, u = m.gate_proj, m.up_proj
+        ops.qmm_dual(x, g.weight, g.scales, g.biases, u.weight, u.scales, u.biases, swiglu=True)
+
+    us = kernel_us(call, 2 * len(layers), torch)
+    N, K = model.cfg.intermediate_size, model.cfg.hidden_size
+    fl = 2 * 2 * PROMPT * N * K
+    tf = fl / us / 1e6
+    traffic = None
+    tf_file = ROOT / "profiles" / "qmm_dual_swiglu_traffic.json"
+    if tf_file.exists():
+        traffic = json.loads(tf_file.read_text()).get("hbm_bytes_per_launch")
+    return {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFS, "unit": "TFLOP/s",
+            "frac": round(tf / BF16_PEAK_TFS, 4), "traffic": traffic,
+            "kernel": "qmm_mfma_kernel (dual gate/up + swiglu epilogue)",
+            "shape": f"M={PROMPT} N=2x{N} K={K} 4-bit g64", "avg_us": round(us, 2),
+            "flops_per_launch": fl}
+
+
+def cpu_baseline(model, ids, torch):
+    """Oracle on the host cores: one layer at L=128 + lm_head for one token,
+    scaled to 36 layers."""
+    import numpy as np
+
+    import oracle
+
+    def lin(m):
+        return (m.weight.cpu().numpy().view(np.uint32), m.scales.float().cpu().numpy(),
+                m.biases.float().cpu().numpy())
+
+    def vec(t):
+        return t.float().cpu().numpy()
+
+    cfg = model.cfg
+    layer = model.model.layers[0]
+    layer = layer.wrapped if hasattr(layer, "wrapped") else layer
+    a, m = layer.self_attn, layer.mlp
+    W = {"q_proj": lin(a.q_proj), "k_proj": lin(a.k_proj), "v_proj": lin(a.v_proj),
+         "o_proj": lin(a.o_proj), "gate_proj": lin(m.gate_proj), "up_proj": lin(m.up_proj),
+         "down_proj": lin(m.down_proj), "q_norm": vec(a.q_norm.weight),
+         "k_norm": vec(a.k_norm.weight), "input_layernorm": vec(layer.input_layernorm.weight),
+         "post_attention_layernorm": vec(layer.post_attention_layernorm.weight)}
+    emb = model.model.embed_tokens
+    E = (emb.weight.cpu().numpy().view(np.uint32), emb.scales.float().cpu().numpy(),
+         emb.biases.float().cpu().numpy())
+    r = np.random.Generator(np.random.PCG64(5))
+    x = oracle.round_to(r.normal(0, 1, (1, PROMPT, cfg.hidden_size)), "bfloat16")
+    kc = np.zeros((1, cfg.num_key_value_heads, PROMPT, cfg.head_dim), np.float32)
+    vc = np.zeros_like(kc)
+    t0 = time.perf_counter()
+    oracle.qwen3_layer(x, W, cfg, 0, kc, vc)
+    t_layer = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    oracle.qmm_factored(x[:, -1:], *E, cfg.group_size, cfg.bits, "bfloat16")
+    t_head = time.perf_counter() - t0
+    total = cfg.num_hidden_layers * t_layer + t_head
+    cores = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit():
+        cores = min(cores, int(omp))
+    return {"value": round(PROMPT / total, 2), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"oracle: 1 of {cfg.num_hidden_layers} decoder layers at L={PROMPT} "
+                      f"({t_layer:.2f} s) + lm_head for 1 token ({t_head:.2f} s), scaled to the "
+                      f"{cfg.num_hidden_layers}-layer model; numpy float64 BLAS for M=128 "
+                      "projections, C/OpenMP factored qmm for the lm_head; MLX CPU backend "
+                      "unavailable (mlx not installed, no network)"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              "(every box in this run has one MI355X; the multi-GPU sharding is a design note)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from autotuner_runtime import hip, ops
+    from workloads import qwen3
+
+    hip.lib()  # fail loudly if the HIP library is missing
+    cfg = qwen3.Qwen3Config()
+    model = qwen3.build(cfg, seed=0)
+    qwen3.install_regions(model)
+    ids = qwen3.tokens(1, PROMPT, cfg.vocab_size)
+    caches = model.make_cache(PROMPT)
+
+    def step():
+        for c in caches:
+            c.offset = 0
+        logits = model(ids, caches)
+        return ops.argmax(logits.reshape(1, -1))
+
+    g, tok = graph_of(step, torch)
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    token = int(tok.item())
+
+    roof = dominant_kernel(model, torch, ops)
+    qmm = qmm_config2(torch, ops)
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(model, ids, torch)
+    line = {
+        "metric": "prefill tok/s Qwen3-4B-shape 4-bit @128 tok; qmm HBM GB/s and MFMA % of peak",
+        "value": round(PROMPT / (ms / 1000.0), 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "config 4: Qwen3-4B-shaped model, 36 layers, 4-bit g64, tied "
+                               "V=151936, prefill of 128 seeded token ids (lm_head on the last "
+                               "position), one HIP-graph replay per step",
+                   "global_batch": 1, "seq_len": PROMPT, "parallelism": "single GPU",
+                   "greedy_token": token},
+        "roofline": roof,
+        "qmm": qmm,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -392,3 +392,58 @@ def shortconv(bx, c, w, state, dtype: str):
     conv = round_to(conv, dtype).astype(np.float64)
     out = round_to(np.asarray(c, np.float64) * conv, dtype)
     return out, round_to(pad[:, -2:], dtype)
+
+
+# ----------------------------------------------------------------------------
+# A12: model composition (mlx-lm qwen3 op order, every op's output in T)
+
+
+def _qmm_auto(x, lin, gs, bits, dtype):
+    """MLX routes small M to the factored qmv and larger M to dequantize-then-
+    matmul (stitch.py:74-100); the oracle follows the same split."""
+    wq, s, b = lin
+    M = int(np.prod(x.shape[:-1]))
+    if M <= 8:
+        return qmm_factored(x, wq, s, b, gs, bits, dtype)
+    return quantized_matmul(x, wq, s, b, gs, bits, dtype)
+
+
+def qwen3_layer(x, W: dict, cfg, offset: int, kcache, vcache, dtype: str = "bfloat16"):
+    """One Qwen3 decoder layer (mlx-lm qwen3.py order): h = x + attn(norm(x)),
+    out = h + mlp(norm(h)). W holds (wq, scales, biases) per projection and norm
+    weights; kcache/vcache [1, HK, cap, D] float32 are written at
+    [offset, offset + L). Returns the layer output [1, L, hidden]."""
+    gs, bits, eps = cfg.group_size, cfg.bits, cfg.rms_norm_eps
+    H, HK, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    L = x.shape[1]
+    xn = rms_norm(x, W["input_layernorm"], eps, dtype)
+    q = _qmm_auto(xn, W["q_proj"], gs, bits, dtype)
+    k = _qmm_auto(xn, W["k_proj"], gs, bits, dtype)
+    v = _qmm_auto(xn, W["v_proj"], gs, bits, dtype)
+    qr = norm_rope(q, W["q_norm"], eps, H, D, cfg.rope_theta, offset, dtype)
+    kcache[:, :, offset:offset + L] = norm_rope(k, W["k_norm"], eps, HK, D, cfg.rope_theta,
+                                                offset, dtype)
+    vcache[:, :, offset:offset + L] = norm_rope(v, None, 0.0, HK, 0, 1.0, 0, dtype)
+    o = sdpa(qr, kcache[:, :, :offset + L], vcache[:, :, :offset + L], D ** -0.5, L > 1, dtype)
+    o = np.ascontiguousarray(np.transpose(o, (0, 2, 1, 3))).reshape(1, L, H * D)
+    h = round_to(x.astype(np.float64) + _qmm_auto(o, W["o_proj"], gs, bits, dtype), dtype)
+    hn = rms_norm(h, W["post_attention_layernorm"], eps, dtype)
+    g = _qmm_auto(hn, W["gate_proj"], gs, bits, dtype)
+    u = _qmm_auto(hn, W["up_proj"], gs, bits, dtype)
+    d = _qmm_auto(swiglu(g, u, dtype), W["down_proj"], gs, bits, dtype)
+    return round_to(h.astype(np.float64) + d, dtype)
+
+
+def qwen3_forward(ids, layers: list, embed, final_norm, cfg, offset: int, kcaches, vcaches,
+                  dtype: str = "bfloat16"):
+    """Embedding (dequantized rows) -> layers -> norm of the last position ->
+    tied lm_head. Returns logits [1, 1, vocab] (values of T)."""
+    wq, s, b = embed
+    rows = np.asarray(ids).reshape(-1)
+    q = unpack(wq[rows], cfg.bits).astype(np.float32)
+    h = round_to(np.repeat(s[rows], cfg.group_size, 1) * q + np.repeat(b[rows], cfg.group_size, 1),
+                 dtype)[None]
+    for i, W in enumerate(layers):
+        h = qwen3_layer(h, W, cfg, offset, kcaches[i], vcaches[i], dtype)
+    hn = rms_norm(h[:, -1:], final_norm, cfg.rms_norm_eps, dtype)
+    return qmm_factored(hn, wq, s, b, cfg.group_size, cfg.bits, dtype)
