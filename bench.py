@@ -2,7 +2,7 @@
 
 `python bench.py [--gpus 1] [--steps K] [--warmup W]` prints ONE JSON line.
 
-A step is one prefill forward of BASELINE config 4's model (36 decoder layers,
+A step is one prefill forward of the benchmark's config 4 model (36 decoder layers,
 hidden 2560, 32/8 heads of 128, SwiGLU 9728, tied quantized embedding/lm_head
 V = 151936, every projection 4-bit affine group 64; random seeded weights and
 token ids) over 128 tokens: embedding gather, 36 layers with the region cuts
@@ -14,7 +14,7 @@ Also measured live, with HIP events on the stream the kernels run on:
   - roofline: the dominant kernel (the M=128 gate/up qmm region of the model,
     the largest GEMM) -- algorithmic flops per launch / average duration,
     against MI355X's dense bf16 MFMA peak (2.5 PFLOP/s);
-  - qmm: BASELINE config 2 (x[M, 2560] @ W[9728, 2560]^T, 4-bit g64) at M=1
+  - qmm: the benchmark's config 2 (x[M, 2560] @ W[9728, 2560]^T, 4-bit g64) at M=1
     (HBM GB/s vs 8 TB/s) and M=128 (TFLOP/s vs the MFMA peak), rotating more
     weight copies than the 256 MB Infinity Cache holds;
   - cpu_baseline: the CPU oracle (the port; MLX is not installed) on a bounded
@@ -27,6 +27,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -129,10 +130,13 @@ def dominant_kernel(model, torch, ops):
     N, K = model.cfg.intermediate_size, model.cfg.hidden_size
     fl = 2 * 2 * PROMPT * N * K
     tf = fl / us / 1e6
+    # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    # passes (calibrated against a copy kernel); null when absent
     traffic = None
-    tf_file = ROOT / "profiles" / "qmm_dual_swiglu_traffic.json"
+    tf_file = ROOT / "profiles" / "qmm_dual_swiglu_m128_hbm_traffic.md"
     if tf_file.exists():
-        traffic = json.loads(tf_file.read_text()).get("hbm_bytes_per_launch")
+        found = re.search(r"^hbm_bytes_per_launch = (\d+)$", tf_file.read_text(), re.M)
+        traffic = int(found.group(1)) if found else None
     return {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFS, "unit": "TFLOP/s",
             "frac": round(tf / BF16_PEAK_TFS, 4), "traffic": traffic,
             "kernel": "qmm_mfma_kernel (dual gate/up + swiglu epilogue)",

@@ -63,7 +63,7 @@ const char *mi_last_error(void);
 int mi_affine_dequant(const uint32_t *w, const void *scales, const void *biases, void *out,
                       int64_t N, int64_t K, int group_size, int bits, int dtype, void *stream);
 
-/* nn.QuantizedEmbedding lookup (mlx-lm glue): rows ids[i] of
+/* nn.QuantizedEmbedding lookup (mlx-lm model glue, the tied embedding): rows ids[i] of
  * the quantized table dequantized into out[i, :] (T [n_ids, K]).
  * ids are int32 or int64 (`ids_are_64`); an id outside [0, N) -> MI_ERR_ARG
  * is not detectable without a sync, so out-of-range ids are clamped to N-1. */

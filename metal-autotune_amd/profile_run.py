@@ -1,0 +1,74 @@
+"""A fixed kernel workload for hardware-counter passes (rocprofv3 --pmc).
+
+    rocprofv3 --pmc FETCH_SIZE -d OUT -o dual -- python metal-autotune_amd/profile_run.py
+    rocprofv3 --pmc WRITE_SIZE -d OUT -o dual -- python metal-autotune_amd/profile_run.py
+
+Runs, eagerly on the current stream:
+
+1. ``copies`` launches of a plain device copy of COPY_BYTES (torch's
+   elementwise copy kernel): the calibration that says how many KiB the
+   FETCH_SIZE / WRITE_SIZE counters report per byte actually moved;
+2. ``reps`` launches of the prefill gate/up region kernel (dual 4-bit qmm with
+   the SwiGLU epilogue, x[128, 2560] against two [9728, 2560] weights, group
+   64) rotating over enough weight sets that they cannot stay in the 256 MB
+   Infinity Cache -- the same kernel and shape bench.py reports in
+   ``roofline``;
+3. the same for a plain qmm at M = 1 (decode GEMV, [9728, 2560]).
+
+Prints one line per phase so the counter rows can be matched to phases by
+kernel name and launch order.
+"""
+
+from __future__ import annotations
+
+import argparse
+import sys
+from pathlib import Path
+
+sys.path.insert(0, str(Path(__file__).resolve().parent))
+
+COPY_BYTES = 256 << 20
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--reps", type=int, default=24)
+    ap.add_argument("--copies", type=int, default=4)
+    args = ap.parse_args()
+
+    import torch
+
+    from autotuner_runtime import hip, ops
+    from workloads.quantize import random_quantized
+
+    hip.lib()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(11)
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device="cuda").uniform_(generator=gen)
+    dst = torch.empty_like(src)
+    for _ in range(args.copies):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"phase copy: {args.copies} x {COPY_BYTES} bytes read + written", flush=True)
+    del src, dst
+
+    N, K, M = 9728, 2560, 128
+    sets = 12  # 12 x 2 x 13.2 MB > 256 MB
+    ws = [(random_quantized(N, K, gen, "cuda"), random_quantized(N, K, gen, "cuda"))
+          for _ in range(sets)]
+    x = torch.randn((1, M, K), generator=gen, device="cuda").to(torch.bfloat16)
+    for i in range(args.reps):
+        g, u = ws[i % sets]
+        ops.qmm_dual(x, *g, *u, swiglu=True)
+    torch.cuda.synchronize()
+    print(f"phase dual: {args.reps} x qmm_dual swiglu M={M} N=2x{N} K={K}", flush=True)
+
+    x1 = x[:, :1].contiguous()
+    for i in range(args.reps):
+        ops.quantized_matmul(x1, *ws[i % sets][i % 2])
+    torch.cuda.synchronize()
+    print(f"phase gemv: {args.reps} x qmm M=1 N={N} K={K}", flush=True)
+
+
+if __name__ == "__main__":
+    main()

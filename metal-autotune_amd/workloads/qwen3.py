@@ -1,4 +1,4 @@
-"""Qwen3-4B-shaped decoder with 4-bit affine weights (BASELINE configs 3 and 4).
+"""Qwen3-4B-shaped decoder with 4-bit affine weights (benchmark configs 3 and 4).
 
 The module tree mirrors mlx-lm's qwen3 model (model.embed_tokens,
 model.layers[i].self_attn.{q,k,v,o}_proj / q_norm / k_norm,

@@ -3,7 +3,7 @@
 Bars: bit-exact for dequant, integer/index outputs and the one-hot cases;
 otherwise the port's region criterion max|c - r| <= tol * max|r| with
 tol 1e-2 for bf16/fp16 and 1e-5 for fp32 (numeric.max_abs_normalised).
-Shapes are BASELINE config 2 (x[M, 2560] @ W[9728, 2560]^T, M in 1/16/128),
+Shapes are the benchmark's config 2 (x[M, 2560] @ W[9728, 2560]^T, M in 1/16/128),
 the Qwen3/LFM2 projection shapes, and ragged edges.
 """
 
@@ -73,7 +73,7 @@ def test_quantized_embedding_gathers_dequantized_rows():
 
 @pytest.mark.parametrize("M", [1, 2, 5, 8, 9, 16, 33, 64, 100, 128, 300])
 def test_qmm_config2_shape(M):
-    """BASELINE config 2 shapes (M in 1/16/128) and the GEMV/MFMA switch
+    """Config 2 shapes (M in 1/16/128) and the GEMV/MFMA switch
     points around them."""
     r = rng(200 + M)
     K, N = 2560, 9728
