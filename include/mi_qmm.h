@@ -118,6 +118,19 @@ int mi_qmm_affine_dual(const void *x, const uint32_t *w1, const void *s1, const 
                        int64_t M, int64_t N, int64_t K, int group_size, int bits, int act,
                        int dtype, void *stream);
 
+/* Three quantized projections of one x in one launch: y[i] = x @ dequant(w[i])^T
+ * for i = 0, 1, 2, each T [M, N[i]] -- the attention block's q/k/v projections,
+ * three mx.quantized_matmul calls on the same normed input
+ * (examples/lfm2_5_1_2b_prefill/.../patch/wrappers.py:156,160,164), grouped
+ * like the two-projection region above. Each N[i] must be a multiple of 32.
+ * Results are bit-identical to three mi_qmm_affine calls. w, scales, biases,
+ * y and N are arrays of 3 (host memory; the pointers they hold are device
+ * pointers). */
+int mi_qmm_affine_grouped3(const void *x, const uint32_t *const w[3], const void *const scales[3],
+                           const void *const biases[3], void *const y[3], int64_t M,
+                           const int64_t N[3], int64_t K, int group_size, int bits, int dtype,
+                           void *stream);
+
 /* mx.fast.rms_norm(x, w, eps) over the last axis of a [rows, D] array:
  * y = T(w * T(x * rsqrt(mean(x^2) + eps))). Form of
  * prefill_bk64.stages/1.metal:34-42; restated lower.py:1318-1354. */

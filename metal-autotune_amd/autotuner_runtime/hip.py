@@ -45,6 +45,7 @@ SIGNATURES: dict[str, list] = {
     "mi_qmm_affine_split_gate": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _I, _P],
     "mi_qmm_affine_dual": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _I,
                            _I, _P],
+    "mi_qmm_affine_grouped3": [_P, _P, _P, _P, _P, _I64, _P, _I64, _I, _I, _I, _P],
     "mi_rms_norm": [_P, _P, _P, _I64, _I64, _F, _I, _P],
     "mi_norm_rope": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _F, _F, _I64, _I64,
                      _I64, _I, _P],
@@ -275,6 +276,27 @@ def b_qmm_dual(ins, outs, p):
                                     _stream(x)), "dual qmm")
 
 
+def b_qmm_grouped3(ins, outs, p):
+    """ins: x, then (w, scales, biases) of each of the 3 projections; outs: 3."""
+    if len(ins) != 10 or len(outs) != 3:
+        raise ValueError("grouped qmm takes x + 3 x (w, scales, biases) and gives 3 outputs")
+    x = ins[0]
+    parts = [ins[1 + 3 * i: 4 + 3 * i] for i in range(3)]
+    _require_gpu(x)
+    _contig(x, *ins[1:], *outs)
+    Ns = []
+    for (w, s, b), y in zip(parts, outs):
+        M, N, K, gs, bits = _qmm_dims(x, w, s, b, p)
+        _out_like(y, x, N)
+        Ns.append(N)
+    dt = _act_dtype(x, parts[0][1])
+    ptrs = (ctypes.c_void_p * 3)
+    _check(lib().mi_qmm_affine_grouped3(
+        _ptr(x), ptrs(*[_ptr(w) for w, _, _ in parts]), ptrs(*[_ptr(s) for _, s, _ in parts]),
+        ptrs(*[_ptr(b) for _, _, b in parts]), ptrs(*[_ptr(y) for y in outs]), M,
+        (ctypes.c_int64 * 3)(*Ns), K, gs, bits, dt, _stream(x)), "grouped qmm")
+
+
 def b_rms_norm(ins, outs, p):
     x, w = ins
     (y,) = outs
@@ -389,6 +411,7 @@ BINDINGS: dict[str, Callable] = {
     "mi_qmm_affine_residual_rmsnorm": b_qmm_residual_rmsnorm,
     "mi_qmm_affine_split_gate": b_qmm_split_gate,
     "mi_qmm_affine_dual": b_qmm_dual,
+    "mi_qmm_affine_grouped3": b_qmm_grouped3,
     "mi_rms_norm": b_rms_norm,
     "mi_norm_rope": b_norm_rope,
     "mi_sdpa": b_sdpa,

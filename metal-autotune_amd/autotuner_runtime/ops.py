@@ -95,6 +95,15 @@ def qmm_dual(x, w1, s1, b1, w2, s2, b2, group_size=64, bits=4, swiglu: bool = Fa
     return y1, y2
 
 
+def qmm_grouped3(x, weights, group_size=64, bits=4):
+    """Three projections of one x in one launch: ``weights`` is three
+    (w, scales, biases) triples; returns the three x @ dequant(w)^T."""
+    outs = [_empty((*x.shape[:-1], w.shape[0]), x) for w, _, _ in weights]
+    ins = [x.contiguous()] + [t for triple in weights for t in triple]
+    hip.b_qmm_grouped3(ins, outs, _qp(group_size, bits))
+    return outs
+
+
 # -- A5, A6 ----------------------------------------------------------------
 
 def rms_norm(x, weight, eps: float) -> torch.Tensor:

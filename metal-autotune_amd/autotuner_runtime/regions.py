@@ -124,6 +124,24 @@ def dual_swiglu(kernel_id="dual_swiglu", dtype="bfloat16", group_size=64, bits=4
                          "template": (*_qparams(group_size, bits), ("act", "1"))})
 
 
+def grouped3(kernel_id="grouped3", dtype="bfloat16", group_size=64, bits=4) -> KernelSpec:
+    """[qmm(wq), qmm(wk), qmm(wv)] sharing x -> three outputs (the attention
+    block's projections of the normed input, patch/wrappers.py:156,160,164 of
+    the LFM2 artifact); inputs (x, wq, sq, bq, wk, sk, bk, wv, sv, bv). Each
+    projection's N must be a multiple of 32 (else the original ops run)."""
+    outs = tuple(("in0.shape[0]", "in0.shape[1]", f"in{1 + 3 * i}.shape[0]") for i in range(3))
+    return KernelSpec(
+        kernel_id=kernel_id, name="mi_qmm_affine_grouped3",
+        input_names=tuple(f"in{i}" for i in range(10)), output_names=("out0", "out1", "out2"),
+        source="mi_qmm_affine_grouped3", output_shapes=outs, output_dtypes=(dtype,) * 3,
+        template=_qparams(group_size, bits),
+        fallback_predicate=(
+            "in0.ndim != 3 or "
+            + " or ".join(f"in{1 + 3 * i}.shape[0] % 32 != 0" for i in range(3)) + " or "
+            + " or ".join(_quant_fallback(0, 1 + 3 * i, 2 + 3 * i, 3 + 3 * i, group_size, bits)
+                          for i in range(3))))
+
+
 def residual(kernel_id="residual", dtype="bfloat16", group_size=64, bits=4) -> KernelSpec:
     """[qmm(w2), add] -> resid + x W2^T; inputs (x, w, scales, biases, residual)."""
     return KernelSpec(

@@ -24,15 +24,21 @@
 //    tiles are reduced through LDS in a fixed order (deterministic).
 //
 // Epilogues implement the reference's region cuts: plain store; [qmm, add];
-// [qmm, split(3), mul]; [qmm(w1), qmm(w3)] (two outputs, or swiglu fused).
+// [qmm, split(3), mul]; [qmm(w1), qmm(w3)] (two outputs, or swiglu fused);
+// and three projections sharing x in one launch (EPI_GROUP3: the weights and
+// outputs are concatenated along N and each workgroup's tile lies in one part).
 #include "mi_common.h"
 
 namespace mi {
 namespace {
 
-enum Epi { EPI_STORE = 0, EPI_RESID = 1, EPI_SPLIT3 = 2, EPI_DUAL = 3, EPI_SWIGLU = 4 };
+enum Epi { EPI_STORE = 0, EPI_RESID = 1, EPI_SPLIT3 = 2, EPI_DUAL = 3, EPI_SWIGLU = 4,
+           EPI_GROUP3 = 5 };
 
-constexpr int epi_parts(int e) { return e == EPI_SPLIT3 ? 3 : (e >= EPI_DUAL ? 2 : 1); }
+// weight rows each output element combines (EPI_GROUP3 selects one weight per tile)
+constexpr int epi_parts(int e) {
+    return e == EPI_SPLIT3 ? 3 : ((e == EPI_DUAL || e == EPI_SWIGLU) ? 2 : 1);
+}
 
 struct QParams {
     const void *x;             // T [M, K]
@@ -44,6 +50,8 @@ struct QParams {
     void *y0;                  // T [M, Nout]
     void *y1;                  // T [M, Nout] (EPI_SPLIT3, EPI_DUAL)
     int64_t M, Nout, K;
+    int64_t pn[3];             // EPI_GROUP3: N of each part (Nout = their sum)
+    void *py[3];               // EPI_GROUP3: output of each part, T [M, pn[i]]
     int gs;
     int gs_log2;               // log2(gs): group sizes are powers of two
     int wk;                    // K-split waves (qmm_mfma_kernel)
@@ -61,7 +69,7 @@ template <typename T, int EPI>
 __device__ __forceinline__ void epi1(const QParams &p, int64_t m, int64_t n, const float *acc) {
     T *y0 = (T *)p.y0;
     const int64_t o = m * p.Nout + n;
-    if constexpr (EPI == EPI_STORE) {
+    if constexpr (EPI == EPI_STORE || EPI == EPI_GROUP3) {
         y0[o] = cvt<T>(acc[0]);
     } else if constexpr (EPI == EPI_RESID) {
         y0[o] = cvt<T>((float)((const T *)p.resid)[o] + (float)cvt<T>(acc[0]));
@@ -93,7 +101,7 @@ __device__ __forceinline__ void epi4(const QParams &p, int64_t m, int64_t n,
     }
     const int64_t o = m * p.Nout + n;
     float v[4];
-    if constexpr (EPI == EPI_STORE) {
+    if constexpr (EPI == EPI_STORE || EPI == EPI_GROUP3) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = acc[0][e];
     } else if constexpr (EPI == EPI_RESID) {
@@ -123,6 +131,26 @@ __device__ __forceinline__ void epi4(const QParams &p, int64_t m, int64_t n,
         for (int e = 0; e < 4; ++e) v[e] = swiglu1<T>(acc[0][e], acc[1][e]);
     }
     st8((T *)p.y0 + o, pack4<T>(v));
+}
+
+// EPI_GROUP3: nb is a workgroup's first output feature in the concatenated
+// space. The host guarantees every part's N is a multiple of each tile width,
+// so the whole tile lies in one part: rebind p to that part (weights, output,
+// width) and return nb relative to it. Other epilogues: nb unchanged.
+template <int EPI>
+__device__ __forceinline__ int64_t select_part(QParams &p, int64_t nb) {
+    if constexpr (EPI == EPI_GROUP3) {
+        const int64_t e0 = p.pn[0], e1 = p.pn[0] + p.pn[1];
+        const int part = nb < e0 ? 0 : (nb < e1 ? 1 : 2);
+        const int64_t start = part == 0 ? 0 : (part == 1 ? e0 : e1);
+        p.w[0] = p.w[part];
+        p.s[0] = p.s[part];
+        p.b[0] = p.b[part];
+        p.y0 = p.py[part];
+        p.Nout = p.pn[part];
+        return nb - start;
+    }
+    return nb;
 }
 
 // ---------------------------------------------------------------------------
@@ -157,7 +185,8 @@ __global__ __launch_bounds__(256) void qmv_kernel(QParams p) {
     constexpr int VPC = 4 * VPW;
     const int lane = threadIdx.x & 63;
     const int j = lane & 15;
-    const int64_t n = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 6) * 4 + (lane >> 4);
+    const int64_t n =
+        select_part<EPI>(p, (int64_t)blockIdx.x * 16) + (threadIdx.x >> 6) * 4 + (lane >> 4);
     const int64_t m0 = (int64_t)blockIdx.y * MR;
     const int64_t K = p.K, cpr = K / VPC, G = K / p.gs;
     const int mr = (int)((p.M - m0) < MR ? (p.M - m0) : MR);
@@ -280,7 +309,8 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
     const int64_t K = p.K, words = K / 8, cpr = K / 32, G = K / p.gs;
     float *xsum = (float *)(xs_pairs + MR * words);
     const int lane = threadIdx.x & 63, j = lane & 15;
-    const int64_t n = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 6) * 4 + (lane >> 4);
+    const int64_t n =
+        select_part<EPI>(p, (int64_t)blockIdx.x * 16) + (threadIdx.x >> 6) * 4 + (lane >> 4);
     const int64_t nrow = n < p.Nout ? n : p.Nout - 1;
     const int64_t m0 = (int64_t)blockIdx.y * MR;
     const int mr = (int)((p.M - m0) < MR ? (p.M - m0) : MR);
@@ -455,7 +485,7 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
     const int kw = threadIdx.x >> 6;
     const int h = lane >> 5, r = lane & 31;
     const int64_t K = p.K, G = K / p.gs;
-    const int64_t n_wave = (int64_t)blockIdx.x * (32 * TN);
+    const int64_t n_wave = select_part<EPI>(p, (int64_t)blockIdx.x * (32 * TN));
     const int64_t m_blk = (int64_t)blockIdx.y * (32 * C);
     const int wk = p.wk;
     const int Kw = (int)(K / wk);
@@ -664,16 +694,27 @@ int launch_mfma_cfg(QParams p, int wk, hipStream_t st) {
     return launch_status("quantized matmul (mfma)");
 }
 
+// Tile choice (measured on MI355X over the Qwen3 prefill shapes, M = 128): one
+// 32-feature tile per part (A = P) and 64-token tiles (C = 2) -- the smallest
+// tiles that still reuse each x fragment across two MFMA columns -- give the
+// most workgroups for these narrow-N GEMMs; 32-token tiles when 64-token tiles
+// would leave fewer than 128 workgroups (half the CUs), and 64x128 tiles once
+// the grid exceeds 2048 workgroups (large M), where re-reading x per narrow
+// tile costs more than the lost parallelism.
 // K must split into wk slices of whole 64-value x stages.
 template <typename T, int BITS, int EPI>
 int launch_mfma(const QParams &p, hipStream_t st) {
     constexpr int P = epi_parts(EPI);
-    constexpr int A = (P == 1) ? 2 : P;
     const int64_t stages = p.K / XK;
     const int wk = (stages % 4 == 0) ? 4 : (stages % 2 == 0 ? 2 : 1);
-    if (p.M > 64) return launch_mfma_cfg<T, BITS, A, 4, EPI>(p, wk, st);
-    if (p.M > 32) return launch_mfma_cfg<T, BITS, A, 2, EPI>(p, wk, st);
-    return launch_mfma_cfg<T, BITS, A, 1, EPI>(p, wk, st);
+    const int64_t nt = ceil_div(p.Nout, 32);
+    if constexpr (P == 1) {
+        if (nt * ceil_div(p.M, 64) > 2048 && EPI != EPI_GROUP3)
+            return launch_mfma_cfg<T, BITS, 2, 4, EPI>(p, wk, st);
+    }
+    if (p.M > 32 && nt * ceil_div(p.M, 64) >= 128)
+        return launch_mfma_cfg<T, BITS, P, 2, EPI>(p, wk, st);
+    return launch_mfma_cfg<T, BITS, P, 1, EPI>(p, wk, st);
 }
 
 template <typename T, int EPI>
@@ -813,4 +854,31 @@ extern "C" int mi_qmm_affine_dual(const void *x, const uint32_t *w1, const void 
     p.y1 = y2;
     if (act == MI_ACT_SWIGLU) return run<EPI_SWIGLU>(p, bits, dtype, stream);
     return run<EPI_DUAL>(p, bits, dtype, stream);
+}
+
+extern "C" int mi_qmm_affine_grouped3(const void *x, const uint32_t *const w[3],
+                                      const void *const scales[3], const void *const biases[3],
+                                      void *const y[3], int64_t M, const int64_t N[3], int64_t K,
+                                      int group_size, int bits, int dtype, void *stream) {
+    if (!w || !scales || !biases || !y || !N) return fail(MI_ERR_ARG, "null array argument");
+    int64_t total = 0;
+    for (int i = 0; i < 3; ++i) {
+        if (int e = check_common(x, w[i], scales[i], biases[i], y[i], M, N[i], K, group_size,
+                                 bits, dtype))
+            return e;
+        // every tile width (16 GEMV rows, 32 MFMA features) must divide each part
+        if (N[i] % 32)
+            return fail(MI_ERR_ARG, "grouped qmm needs each N to be a multiple of 32, got %lld",
+                        (long long)N[i]);
+        total += N[i];
+    }
+    QParams p = base_params(x, w[0], scales[0], biases[0], y[0], M, total, K, group_size);
+    for (int i = 0; i < 3; ++i) {
+        p.w[i] = w[i];
+        p.s[i] = scales[i];
+        p.b[i] = biases[i];
+        p.py[i] = y[i];
+        p.pn[i] = N[i];
+    }
+    return run<EPI_GROUP3>(p, bits, dtype, stream);
 }

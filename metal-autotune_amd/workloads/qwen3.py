@@ -183,6 +183,7 @@ class Qwen3Model(nn.Module):
 def layer_specs(cfg: Qwen3Config, dtype: str = "bfloat16") -> dict:
     gs, bits = cfg.group_size, cfg.bits
     return {
+        "qkv": regions.grouped3("qwen3_qkv_proj", dtype, gs, bits),
         "residual_rmsnorm": regions.residual_rmsnorm("qwen3_o_proj_add_norm", dtype, gs, bits,
                                                      cfg.rms_norm_eps),
         "dual_swiglu": regions.dual_swiglu("qwen3_gate_up_swiglu", dtype, gs, bits),
@@ -194,7 +195,8 @@ class Qwen3LayerRegions(ReplayWrapper):
     """The decoder layer with the region cuts spliced in (try_sized, else the
     original ops)."""
 
-    KERNEL_IDS = ["qwen3_o_proj_add_norm", "qwen3_gate_up_swiglu", "qwen3_down_add"]
+    KERNEL_IDS = ["qwen3_qkv_proj", "qwen3_o_proj_add_norm", "qwen3_gate_up_swiglu",
+                  "qwen3_down_add"]
 
     def forward(self, x, cache: KVCache):
         w = self.wrapped
@@ -204,9 +206,10 @@ class Qwen3LayerRegions(ReplayWrapper):
         c = attn.cfg
         B, L, _ = x.shape
         xn = w.input_layernorm(x)
-        q = attn.q_proj(xn)
-        k = attn.k_proj(xn)
-        v = attn.v_proj(xn)
+        projs = (attn.q_proj, attn.k_proj, attn.v_proj)
+        outs = _kernels.try_sized(self._specs["qkv"],
+                                  [xn] + [t for m in projs for t in (m.weight, m.scales, m.biases)])
+        q, k, v = (m(xn) for m in projs) if outs is None else outs
         qr = ops.norm_rope(q, attn.q_norm.weight, c.num_attention_heads, c.rms_norm_eps,
                            c.head_dim, c.rope_theta, cache.offset)
         ops.norm_rope(k, attn.k_norm.weight, c.num_key_value_heads, c.rms_norm_eps, c.head_dim,

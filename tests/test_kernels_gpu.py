@@ -201,6 +201,35 @@ def test_qmm_dual_and_swiglu(M):
     assert torch.equal(sw, ops.swiglu(g, u))
 
 
+@pytest.mark.parametrize("M", [1, 3, 8, 16, 40, 128, 300])
+@pytest.mark.parametrize("bits,dtype", [(4, "bfloat16"), (8, "float16"), (4, "float32")])
+def test_qmm_grouped3_equals_three_launches(M, bits, dtype):
+    """q/k/v in one launch: bit-identical to three mi_qmm_affine calls (the
+    per-element reduction order does not depend on the tile), and within the
+    tolerance of the oracle; parts of unequal width (4096-like / 1024-like)."""
+    r = rng(720 + M + bits)
+    K = 512
+    Ns = (256, 64, 96)
+    x = oracle.round_to(r.normal(0, 1, (1, M, K)), dtype)
+    qs = [_quant(721 + i, n, K, 64, bits, dtype) for i, n in enumerate(Ns)]
+    xd = to_torch(x, dtype)
+    ws = [_dev(*q, dtype) for q in qs]
+    got = ops.qmm_grouped3(xd, ws, 64, bits)
+    for (wq, s, b), w, y in zip(qs, ws, got):
+        sep = ops.quantized_matmul(xd, *w, group_size=64, bits=bits)
+        assert torch.equal(y, sep)
+        _close(y, oracle.quantized_matmul(x, wq, s, b, 64, bits, dtype), dtype,
+               1e-5 if dtype == "float32" else None)
+
+
+def test_qmm_grouped3_rejects_unaligned_parts():
+    K = 256
+    qs = [_quant(730 + i, n, K) for i, n in enumerate((64, 48, 64))]
+    x = to_torch(np.zeros((1, 4, K), np.float32), "bfloat16")
+    with pytest.raises(ValueError, match="multiple of 32"):
+        ops.qmm_grouped3(x, [_dev(*q, "bfloat16") for q in qs])
+
+
 # ------------------------------------------------------------------ A5-A10
 
 
