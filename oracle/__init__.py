@@ -40,6 +40,16 @@ Pins (all in tests/test_oracle.py):
   swiglu, gelu        closed forms (math.erf) on scalars.
   shortconv           direct 3-tap sum against a hand-computed case; state
                       carries the last two rows; chunked == whole sequence.
+  qwen3_layer         op order of mlx-lm's qwen3 decoder (un-vendored; the
+                      reference's tests/fixtures/llama_ish.py:25-39 states the
+                      same residual structure); pinned by structure checks:
+                      zero o_proj/down_proj -> identity exactly; decode at
+                      offset L against a cache filled by the prefix == the
+                      last row of an (L+1)-token prefill, and a wrong offset
+                      fails that bar. Bitwise agreement with MLX's own layer
+                      (its fused-kernel rounding) is parity unpinned.
+  qwen3_forward       no-layer case: tied head over the dequantized table
+                      row of the last id.
 """
 
 from __future__ import annotations

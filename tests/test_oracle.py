@@ -315,3 +315,92 @@ def test_tiny_mlp_bias_path():
     w1 = r.normal(0, 0.02, (16, 8))
     y = oracle.tiny_mlp(x, w1, np.zeros(16), np.zeros((4, 16)), np.full(4, 0.25))
     assert (y == np.float32(0.25)).all()
+
+
+# ---------------------------------------------------------------------- A12
+
+
+def _tiny_cfg():
+    from types import SimpleNamespace
+
+    return SimpleNamespace(group_size=64, bits=4, rms_norm_eps=1e-6, num_attention_heads=4,
+                           num_key_value_heads=2, head_dim=32, rope_theta=1e6)
+
+
+def _tiny_layer(seed, hidden=128, inter=256, zero=()):
+    cfg = _tiny_cfg()
+    r = rng(seed)
+    H, HK, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    shapes = {"q_proj": (H * D, hidden), "k_proj": (HK * D, hidden), "v_proj": (HK * D, hidden),
+              "o_proj": (hidden, H * D), "gate_proj": (inter, hidden), "up_proj": (inter, hidden),
+              "down_proj": (hidden, inter)}
+    W = {}
+    for name, (n, k) in shapes.items():
+        wq, s, b = oracle.quantize_affine(r.normal(0, 0.05, (n, k)).astype(np.float32), 64, 4,
+                                          "bfloat16")
+        if name in zero:
+            s, b = np.zeros_like(s), np.zeros_like(b)
+        W[name] = (wq, s, b)
+    for name, d in (("q_norm", D), ("k_norm", D), ("input_layernorm", hidden),
+                    ("post_attention_layernorm", hidden)):
+        W[name] = oracle.round_to(1 + 0.1 * r.normal(0, 1, d), "bfloat16")
+    return cfg, W
+
+
+def _caches(cfg, cap=16):
+    kc = np.zeros((1, cfg.num_key_value_heads, cap, cfg.head_dim), np.float32)
+    return kc, np.zeros_like(kc)
+
+
+def test_layer_residual_structure():
+    """o_proj and down_proj dequantizing to zero leave both residual adds
+    with nothing to add: the layer is the identity, exactly (a missing or
+    doubled residual, or a norm applied to the stream, fails)."""
+    cfg, W = _tiny_layer(40, zero=("o_proj", "down_proj"))
+    x = oracle.round_to(rng(41).normal(0, 1, (1, 5, 128)), "bfloat16")
+    kc, vc = _caches(cfg)
+    assert np.array_equal(oracle.qwen3_layer(x, W, cfg, 0, kc, vc), x)
+
+
+def test_layer_decode_with_cache_equals_prefill_last_row():
+    """A prefix through the layer fills the cache; the next token decoded at
+    offset 5 against that cache matches the last row of a 6-token prefill
+    (positions, rope offset, cache rows and the causal mask line up). The
+    two take different qmm orderings (factored at M=1, dequantize-first at
+    M=6), so agreement is to bf16 rounding."""
+    cfg, W = _tiny_layer(42)
+    seq = oracle.round_to(rng(43).normal(0, 1, (1, 6, 128)), "bfloat16")
+    kc, vc = _caches(cfg)
+    full = oracle.qwen3_layer(seq, W, cfg, 0, kc, vc)
+    kc2, vc2 = _caches(cfg)
+    oracle.qwen3_layer(seq[:, :5], W, cfg, 0, kc2, vc2)
+    last = oracle.qwen3_layer(seq[:, 5:], W, cfg, 5, kc2, vc2)
+    err = np.abs(last - full[:, 5:]).max() / np.abs(full[:, 5:]).max()
+    assert err < 1e-2
+    np.testing.assert_allclose(kc2[:, :, :6], kc[:, :, :6], rtol=0, atol=0.05)
+    # a wrong offset (rope at position 0 instead of 5) is far outside that bar
+    kc3, vc3 = _caches(cfg)
+    oracle.qwen3_layer(seq[:, :5], W, cfg, 0, kc3, vc3)
+    kc3[:, :, 5:] = 0
+    wrong = oracle.qwen3_layer(seq[:, 5:], W, cfg, 0, kc3, vc3)
+    assert np.abs(wrong - full[:, 5:]).max() / np.abs(full[:, 5:]).max() > 1e-2
+
+
+def test_forward_embedding_gather_and_tied_head():
+    """qwen3_forward with no layers: the embedding rows are the dequantized
+    table rows and the logits are the factored qmm of the normed last row
+    against the same table."""
+    cfg = _tiny_cfg()
+    r = rng(44)
+    V, hidden = 96, 128
+    emb = oracle.quantize_affine(r.normal(0, 0.05, (V, hidden)).astype(np.float32), 64, 4,
+                                 "bfloat16")
+    fn = oracle.round_to(1 + 0.1 * r.normal(0, 1, hidden), "bfloat16")
+    ids = np.array([[3, 95, 0, 17]])
+    logits = oracle.qwen3_forward(ids, [], emb, fn, cfg, 0, [], [])
+    table = oracle.dequantize(*emb, 64, 4, "bfloat16")
+    hn = oracle.rms_norm(table[ids[0, -1]][None, None], fn, cfg.rms_norm_eps, "bfloat16")
+    want = oracle.round_to(hn.astype(np.float64) @ table.astype(np.float64).T, "bfloat16")
+    assert logits.shape == (1, 1, V)
+    err = np.abs(logits - want).max() / np.abs(want).max()
+    assert err < 1e-2
