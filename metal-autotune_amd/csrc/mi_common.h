@@ -70,9 +70,17 @@ __device__ __forceinline__ typename Vec<T>::x8 dequant8(uint32_t w0, uint32_t w1
                                                        float b) {
     typename Vec<T>::x8 r;
     if constexpr (BITS == 4) {
+        // even nibbles to the bytes of lo, odd nibbles to the bytes of hi, so
+        // each value converts with one v_cvt_f32_ubyte{0..3}; the empty asm
+        // hides the masks, which would otherwise be folded back into one
+        // shift-and-mask per nibble
+        uint32_t lo = w0 & 0x0F0F0F0Fu, hi = (w0 >> 4) & 0x0F0F0F0Fu;
+        asm("" : "+v"(lo), "+v"(hi));
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            r[i] = (T)__builtin_fmaf(s, (float)((w0 >> (4 * i)) & 15u), b);
+        for (int k = 0; k < 4; ++k) {
+            r[2 * k] = (T)__builtin_fmaf(s, (float)((lo >> (8 * k)) & 255u), b);
+            r[2 * k + 1] = (T)__builtin_fmaf(s, (float)((hi >> (8 * k)) & 255u), b);
+        }
     } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {

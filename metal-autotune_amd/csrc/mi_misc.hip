@@ -96,30 +96,73 @@ __global__ __launch_bounds__(256) void linear_f32_kernel(const float *__restrict
     y[m * N + n] = acc;
 }
 
-template <typename T>
-__global__ __launch_bounds__(256) void argmax_kernel(const T *__restrict__ x,
-                                                     int32_t *__restrict__ out, int64_t V) {
-    __shared__ float sv[4];
-    __shared__ int64_t si[4];
+// Greedy argmax: one 1024-thread workgroup per row. Each thread keeps the
+// first maximum of the elements it scans (in increasing index order); the
+// (value, index) pairs are then combined with the lowest index winning a tie.
+// NaN never wins (every comparison with it is false); a row with no non-NaN
+// value gives 0. VEC: the row is read in 16-byte chunks, 8 chunks in flight
+// per thread (rows must be 16-byte aligned and V a multiple of the chunk).
+constexpr int AM_THREADS = 1024;
+constexpr int AM_BATCH = 8;
+
+__device__ __forceinline__ void am_take(float v, int64_t i, float &best, int64_t &bi) {
+    if (v > best || (bi < 0 && !isnan(v))) {
+        best = v;
+        bi = i;
+    }
+}
+
+__device__ __forceinline__ void am_merge(float ov, int64_t oi, float &best, int64_t &bi) {
+    if (oi >= 0 && (bi < 0 || ov > best || (ov == best && oi < bi))) {
+        best = ov;
+        bi = oi;
+    }
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(AM_THREADS) void argmax_kernel(const T *__restrict__ x,
+                                                            int32_t *__restrict__ out, int64_t V) {
+    constexpr int E = 16 / (int)sizeof(T);  // values per 16-byte chunk
+    constexpr int NW = AM_THREADS / 64;
+    __shared__ float sv[NW];
+    __shared__ int64_t si[NW];
     const T *row = x + (int64_t)blockIdx.x * V;
     float best = -INFINITY;
     int64_t bi = -1;
-    for (int64_t i = threadIdx.x; i < V; i += 256) {
-        const float v = (float)row[i];
-        if (v > best || (bi < 0 && !isnan(v))) {
-            best = v;
-            bi = i;
+    if constexpr (VEC) {
+        const int64_t nc = V / E;
+        for (int64_t c0 = threadIdx.x; c0 < nc; c0 += (int64_t)AM_THREADS * AM_BATCH) {
+            uint4 d[AM_BATCH];
+#pragma unroll
+            for (int u = 0; u < AM_BATCH; ++u) {
+                const int64_t c = c0 + (int64_t)u * AM_THREADS;
+                d[u] = ld16(row + (c < nc ? c : nc - 1) * E);  // clamped: always in bounds
+            }
+#pragma unroll
+            for (int u = 0; u < AM_BATCH; ++u) {
+                const int64_t c = c0 + (int64_t)u * AM_THREADS;
+                if (c >= nc) break;
+                float f[E];
+                if constexpr (sizeof(T) == 2) {
+                    unpack8<T>(d[u], f);
+                } else {
+                    f[0] = __uint_as_float(d[u].x);
+                    f[1] = __uint_as_float(d[u].y);
+                    f[2] = __uint_as_float(d[u].z);
+                    f[3] = __uint_as_float(d[u].w);
+                }
+#pragma unroll
+                for (int e = 0; e < E; ++e) am_take(f[e], c * E + e, best, bi);
+            }
         }
+    } else {
+        for (int64_t i = threadIdx.x; i < V; i += AM_THREADS) am_take((float)row[i], i, best, bi);
     }
-    // (value, index) max with lowest index on ties; -1 = no candidate
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(best, o, 64);
         const int64_t oi = __shfl_xor(bi, o, 64);
-        if (oi >= 0 && (bi < 0 || ov > best || (ov == best && oi < bi))) {
-            best = ov;
-            bi = oi;
-        }
+        am_merge(ov, oi, best, bi);
     }
     const int wave = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) {
@@ -128,11 +171,7 @@ __global__ __launch_bounds__(256) void argmax_kernel(const T *__restrict__ x,
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w2 = 1; w2 < 4; ++w2)
-            if (si[w2] >= 0 && (bi < 0 || sv[w2] > best || (sv[w2] == best && si[w2] < bi))) {
-                best = sv[w2];
-                bi = si[w2];
-            }
+        for (int w2 = 1; w2 < NW; ++w2) am_merge(sv[w2], si[w2], best, bi);
         out[blockIdx.x] = (int32_t)(bi < 0 ? 0 : bi);
     }
 }
@@ -208,11 +247,21 @@ extern "C" int mi_argmax(const void *x, int32_t *out, int64_t rows, int64_t V, i
     if (rows == 0) return MI_OK;
     if (!x || !out) return fail(MI_ERR_ARG, "null pointer");
     hipStream_t st = as_stream(stream);
+    const int esize = dtype == MI_F32 ? 4 : 2;
+    const bool vec = aligned(x, 16) && (V * esize) % 16 == 0;
+#define MI_AM(TT)                                                                               \
+    do {                                                                                        \
+        if (vec)                                                                                \
+            argmax_kernel<TT, true><<<(unsigned)rows, AM_THREADS, 0, st>>>((const TT *)x, out, V); \
+        else                                                                                    \
+            argmax_kernel<TT, false><<<(unsigned)rows, AM_THREADS, 0, st>>>((const TT *)x, out, V); \
+    } while (0)
     if (dtype == MI_BF16)
-        argmax_kernel<bf16><<<(unsigned)rows, 256, 0, st>>>((const bf16 *)x, out, V);
+        MI_AM(bf16);
     else if (dtype == MI_F16)
-        argmax_kernel<f16><<<(unsigned)rows, 256, 0, st>>>((const f16 *)x, out, V);
+        MI_AM(f16);
     else
-        argmax_kernel<float><<<(unsigned)rows, 256, 0, st>>>((const float *)x, out, V);
+        MI_AM(float);
+#undef MI_AM
     return launch_status("argmax");
 }

@@ -64,11 +64,49 @@ template <typename T> __device__ __forceinline__ float swiglu1(float g, float u)
     return act * (float)cvt<T>(u);
 }
 
+// The arrays one workgroup reads and writes, held as scalar fields with
+// select accessors: the kernels never modify the QParams argument (a modified
+// copy whose arrays are indexed in loops ends up in scratch memory).
+struct Bound {
+    const uint32_t *w0, *w1, *w2;
+    const void *s0, *s1, *s2;
+    const void *b0, *b1, *b2;
+    int64_t o0, o1, o2;  // row offset of each part inside its weight
+    void *y0;            // this workgroup's output
+    int64_t Nout;        // its width
+    __device__ const uint32_t *w(int i) const { return i == 0 ? w0 : (i == 1 ? w1 : w2); }
+    __device__ const void *s(int i) const { return i == 0 ? s0 : (i == 1 ? s1 : s2); }
+    __device__ const void *b(int i) const { return i == 0 ? b0 : (i == 1 ? b1 : b2); }
+    __device__ int64_t noff(int i) const { return i == 0 ? o0 : (i == 1 ? o1 : o2); }
+};
+
+// Binds a workgroup whose first output feature is nb. EPI_GROUP3: the three
+// weights and outputs are concatenated along N and the host guarantees every
+// part's N is a multiple of each tile width, so the whole tile lies in one
+// part: bind that part as part 0 and make nb relative to it.
+template <int EPI>
+__device__ __forceinline__ Bound bind(const QParams &p, int64_t &nb) {
+    Bound q = {p.w[0], p.w[1], p.w[2], p.s[0], p.s[1], p.s[2], p.b[0], p.b[1], p.b[2],
+               p.noff[0], p.noff[1], p.noff[2], p.y0, p.Nout};
+    if constexpr (EPI == EPI_GROUP3) {
+        const int64_t e0 = p.pn[0], e1 = p.pn[0] + p.pn[1];
+        const bool p0 = nb < e0, p1 = !p0 && nb < e1;
+        nb -= p0 ? 0 : (p1 ? e0 : e1);
+        q.w0 = p0 ? p.w[0] : (p1 ? p.w[1] : p.w[2]);
+        q.s0 = p0 ? p.s[0] : (p1 ? p.s[1] : p.s[2]);
+        q.b0 = p0 ? p.b[0] : (p1 ? p.b[1] : p.b[2]);
+        q.y0 = p0 ? p.py[0] : (p1 ? p.py[1] : p.py[2]);
+        q.Nout = p0 ? p.pn[0] : (p1 ? p.pn[1] : p.pn[2]);
+    }
+    return q;
+}
+
 // Epilogue for one output element (m, n) of the output sub-space.
 template <typename T, int EPI>
-__device__ __forceinline__ void epi1(const QParams &p, int64_t m, int64_t n, const float *acc) {
-    T *y0 = (T *)p.y0;
-    const int64_t o = m * p.Nout + n;
+__device__ __forceinline__ void epi1(const QParams &p, const Bound &bd, int64_t m, int64_t n,
+                                     const float *acc) {
+    T *y0 = (T *)bd.y0;
+    const int64_t o = m * bd.Nout + n;
     if constexpr (EPI == EPI_STORE || EPI == EPI_GROUP3) {
         y0[o] = cvt<T>(acc[0]);
     } else if constexpr (EPI == EPI_RESID) {
@@ -87,19 +125,19 @@ __device__ __forceinline__ void epi1(const QParams &p, int64_t m, int64_t n, con
 
 // Epilogue for 4 consecutive output features n..n+3 of token m; acc[part][e].
 template <typename T, int EPI, int P>
-__device__ __forceinline__ void epi4(const QParams &p, int64_t m, int64_t n,
+__device__ __forceinline__ void epi4(const QParams &p, const Bound &bd, int64_t m, int64_t n,
                                      const float (&acc)[P][4]) {
-    if (m >= p.M || n >= p.Nout) return;
-    if (n + 4 > p.Nout || (p.Nout & 3)) {  // ragged tail: element stores
-        for (int e = 0; e < 4 && n + e < p.Nout; ++e) {
+    if (m >= p.M || n >= bd.Nout) return;
+    if (n + 4 > bd.Nout || (bd.Nout & 3)) {  // ragged tail: element stores
+        for (int e = 0; e < 4 && n + e < bd.Nout; ++e) {
             float a[P];
 #pragma unroll
             for (int q = 0; q < P; ++q) a[q] = acc[q][e];
-            epi1<T, EPI>(p, m, n + e, a);
+            epi1<T, EPI>(p, bd, m, n + e, a);
         }
         return;
     }
-    const int64_t o = m * p.Nout + n;
+    const int64_t o = m * bd.Nout + n;
     float v[4];
     if constexpr (EPI == EPI_STORE || EPI == EPI_GROUP3) {
 #pragma unroll
@@ -130,27 +168,7 @@ __device__ __forceinline__ void epi4(const QParams &p, int64_t m, int64_t n,
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = swiglu1<T>(acc[0][e], acc[1][e]);
     }
-    st8((T *)p.y0 + o, pack4<T>(v));
-}
-
-// EPI_GROUP3: nb is a workgroup's first output feature in the concatenated
-// space. The host guarantees every part's N is a multiple of each tile width,
-// so the whole tile lies in one part: rebind p to that part (weights, output,
-// width) and return nb relative to it. Other epilogues: nb unchanged.
-template <int EPI>
-__device__ __forceinline__ int64_t select_part(QParams &p, int64_t nb) {
-    if constexpr (EPI == EPI_GROUP3) {
-        const int64_t e0 = p.pn[0], e1 = p.pn[0] + p.pn[1];
-        const int part = nb < e0 ? 0 : (nb < e1 ? 1 : 2);
-        const int64_t start = part == 0 ? 0 : (part == 1 ? e0 : e1);
-        p.w[0] = p.w[part];
-        p.s[0] = p.s[part];
-        p.b[0] = p.b[part];
-        p.y0 = p.py[part];
-        p.Nout = p.pn[part];
-        return nb - start;
-    }
-    return nb;
+    st8((T *)bd.y0 + o, pack4<T>(v));
 }
 
 // ---------------------------------------------------------------------------
@@ -185,8 +203,9 @@ __global__ __launch_bounds__(256) void qmv_kernel(QParams p) {
     constexpr int VPC = 4 * VPW;
     const int lane = threadIdx.x & 63;
     const int j = lane & 15;
-    const int64_t n =
-        select_part<EPI>(p, (int64_t)blockIdx.x * 16) + (threadIdx.x >> 6) * 4 + (lane >> 4);
+    int64_t nb = (int64_t)blockIdx.x * 16;
+    const Bound bd = bind<EPI>(p, nb);
+    const int64_t n = nb + (threadIdx.x >> 6) * 4 + (lane >> 4);
     const int64_t m0 = (int64_t)blockIdx.y * MR;
     const int64_t K = p.K, cpr = K / VPC, G = K / p.gs;
     const int mr = (int)((p.M - m0) < MR ? (p.M - m0) : MR);
@@ -200,16 +219,16 @@ __global__ __launch_bounds__(256) void qmv_kernel(QParams p) {
 
     // out-of-range rows/tokens read clamped, valid addresses (no branch around
     // loads); their sums are never stored
-    const int64_t nrow = n < p.Nout ? n : p.Nout - 1;
+    const int64_t nrow = n < bd.Nout ? n : bd.Nout - 1;
     const uint32_t *wr[P];
     const T *sr[P];
     const T *br[P];
 #pragma unroll
     for (int q = 0; q < P; ++q) {
-        const int64_t row = p.noff[q] + nrow;
-        wr[q] = p.w[q] + row * (K / VPW);
-        sr[q] = (const T *)p.s[q] + row * G;
-        br[q] = (const T *)p.b[q] + row * G;
+        const int64_t row = bd.noff(q) + nrow;
+        wr[q] = bd.w(q) + row * (K / VPW);
+        sr[q] = (const T *)bd.s(q) + row * G;
+        br[q] = (const T *)bd.b(q) + row * G;
     }
 #pragma unroll 2
     for (int64_t c = j; c < cpr; c += 16) {
@@ -254,14 +273,14 @@ __global__ __launch_bounds__(256) void qmv_kernel(QParams p) {
             v += __shfl_xor(v, 1, 16);
             acc[q][m] = v;
         }
-    if (j == 0 && n < p.Nout) {
+    if (j == 0 && n < bd.Nout) {
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             if (m < mr) {
                 float a[P];
 #pragma unroll
                 for (int q = 0; q < P; ++q) a[q] = acc[q][m];
-                epi1<T, EPI>(p, m0 + m, n, a);
+                epi1<T, EPI>(p, bd, m0 + m, n, a);
             }
         }
     }
@@ -309,9 +328,10 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
     const int64_t K = p.K, words = K / 8, cpr = K / 32, G = K / p.gs;
     float *xsum = (float *)(xs_pairs + MR * words);
     const int lane = threadIdx.x & 63, j = lane & 15;
-    const int64_t n =
-        select_part<EPI>(p, (int64_t)blockIdx.x * 16) + (threadIdx.x >> 6) * 4 + (lane >> 4);
-    const int64_t nrow = n < p.Nout ? n : p.Nout - 1;
+    int64_t nb = (int64_t)blockIdx.x * 16;
+    const Bound bd = bind<EPI>(p, nb);
+    const int64_t n = nb + (threadIdx.x >> 6) * 4 + (lane >> 4);
+    const int64_t nrow = n < bd.Nout ? n : bd.Nout - 1;
     const int64_t m0 = (int64_t)blockIdx.y * MR;
     const int mr = (int)((p.M - m0) < MR ? (p.M - m0) : MR);
 
@@ -320,10 +340,10 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
     const T *br[P];
 #pragma unroll
     for (int q = 0; q < P; ++q) {
-        const int64_t row = p.noff[q] + nrow;
-        wr[q] = p.w[q] + row * (K / 8);
-        sr[q] = (const T *)p.s[q] + row * G;
-        br[q] = (const T *)p.b[q] + row * G;
+        const int64_t row = bd.noff(q) + nrow;
+        wr[q] = bd.w(q) + row * (K / 8);
+        sr[q] = (const T *)bd.s(q) + row * G;
+        br[q] = (const T *)bd.b(q) + row * G;
     }
 
     // stage x rows as pairs (e[i], e[i+4]) of each 8-value block
@@ -415,14 +435,14 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
             v += __shfl_xor(v, 1, 16);
             acc[q][m] = v;
         }
-    if (j == 0 && n < p.Nout) {
+    if (j == 0 && n < bd.Nout) {
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             if (m < mr) {
                 float a[P];
 #pragma unroll
                 for (int q = 0; q < P; ++q) a[q] = acc[q][m];
-                epi1<T, EPI>(p, m0 + m, n, a);
+                epi1<T, EPI>(p, bd, m0 + m, n, a);
             }
         }
     }
@@ -446,18 +466,26 @@ template <> struct Mfma<f16> {
 // A: 32-row weight tiles per wave (one per part when P > 1); C: 32-token
 // tiles per wave; WK: waves per workgroup, each owning a 1/wk slice of K.
 //
-// x reaches the MFMAs through LDS: each wave streams its own K slice of the
-// token tile into its own double-buffered LDS region with direct-to-LDS DMA
-// (global_load_lds_dwordx4), 8 rows x 128 bytes per instruction, so every x
-// cache line is fetched once. (Loading x fragments straight into registers
-// makes each lane read a different token row; with four waves the per-step
-// working set overflows the 32 KB L1 and every 16-byte use re-fetches a line.)
-// The 16-byte chunks of a row are XOR-swizzled by (row >> 1) & 7 so a
-// 16-lane ds_read_b128 group covers 16 distinct bank groups. Weight fragments
-// go straight to registers (each element is used by exactly one lane).
+// Everything a stage needs reaches the wave through LDS by direct-to-LDS DMA
+// (buffer_load ... lds), into a ring of PIPE stage slots per wave:
+//  * the x tile of the stage, 8 token rows x 128 bytes per instruction, so
+//    every x cache line is fetched once (loading x fragments straight into
+//    registers makes each lane read a different token row, and with four
+//    waves the per-step working set overflows the 32 KB L1). The 16-byte
+//    chunks of a row are XOR-swizzled by (row >> 1) & 7 so a 16-lane
+//    ds_read_b128 group covers 16 distinct bank groups;
+//  * each lane's 16-byte weight chunk, per part and super-step (lane l's
+//    chunk lands at l * 16, where the same lane reads it back);
+//  * each lane's scale and bias (2-byte DMA writes one zero-extended dword
+//    per lane, at l * 4).
+// With no load result held in registers across stages, the explicit vmcnt
+// at the top of a stage is the only wait the loop needs, and the addresses
+// are a per-lane 32-bit offset plus a scalar stage offset (no VALU address
+// arithmetic in the loop).
 constexpr int XK = 64;  // k values per x stage (128 bytes of a token row)
+constexpr int LDS_PER_CU = 160 * 1024;
 
-template <typename T, int BITS, int A, int C, int WK>
+template <typename T, int BITS, int A, int C, int WK, int PIPE>
 struct MfmaShape {
     static constexpr int VPW = 32 / BITS;  // values per word
     static constexpr int VPC = 4 * VPW;    // values per 16-byte weight chunk (per lane half)
@@ -465,15 +493,64 @@ struct MfmaShape {
     static constexpr int SS = 2 * VPC;     // k per super-step
     static constexpr int SPS = XK / SS;    // super-steps per x stage
     static constexpr int ROWS = 32 * C;    // token rows per stage
-    static constexpr int STAGE = ROWS * 128;                          // bytes per x stage
-    static constexpr int XBYTES = WK * 2 * STAGE;                     // x staging
+    // Several weight tiles per wave (A > 1): their chunks, scales and biases
+    // are prefetched one stage ahead into registers instead of the ring, which
+    // keeps the ring small enough for two workgroups per CU.
+    static constexpr bool WREG = A > 1;
+    static constexpr int XST = ROWS * 128;                           // x tile bytes per stage
+    static constexpr int WST = WREG ? 0 : A * SPS * 1024;            // weight chunks per stage
+    static constexpr int SBST = WREG ? 0 : 2 * A * SPS * 256;        // scale and bias dwords
+    static constexpr int STAGE = XST + WST + SBST;      // one ring slot
+    static constexpr int XBYTES = WK * PIPE * STAGE;                  // stage rings
     static constexpr int RBYTES = (WK - 1) * A * C * 16 * 64 * 4;     // K-split reduction
     static constexpr int LDS = XBYTES > RBYTES ? XBYTES : RBYTES;
+    // DMA instructions a lane issues per stage: x, weights, scales, biases
+    static constexpr int OPS = ROWS / 8 + (WREG ? 0 : 3 * A * SPS);
+    // vmcnt at the top of a stage: the loads of the PIPE - 2 stages issued
+    // after it may still be in flight (vmcnt decrements in issue order)
+    static constexpr int VMCNT = (PIPE - 2) * OPS;
+    static_assert(PIPE >= 2 && PIPE <= 4 && VMCNT < 64, "vmcnt is a 6-bit count");
+    static_assert(!WREG || PIPE == 2, "register-prefetched weights run one stage ahead");
+    static_assert(LDS <= LDS_PER_CU, "stage rings exceed the LDS of a CU");
 };
 
-template <typename T, int BITS, int A, int C, int WK, int EPI>
+// A raw buffer resource over [base, base + bytes): 32-bit offsets, and reads
+// past the end return zero instead of touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+    // dword 3: 32-bit data format (gfx9 raw buffer access)
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+// Stages in flight per wave: the deepest ring (at most MI_QMM_MAX_PIPE, a
+// build-time tuning knob) whose four waves' slots fit the LDS of a CU.
+// Measured on MI355X at the Qwen3 prefill shapes, two stages win: a third
+// stage buys less than the second resident workgroup per CU it costs (two
+// waves per SIMD overlap one wave's dequant VALU with the other's MFMAs).
+#ifndef MI_QMM_MAX_PIPE
+#define MI_QMM_MAX_PIPE 2
+#endif
+template <typename T, int BITS, int A, int C> constexpr int mfma_pipe() {
+    typedef MfmaShape<T, BITS, A, C, 4, 2> Sh2;
+    if constexpr (Sh2::WREG) return 2;
+    constexpr int slot = Sh2::STAGE;
+    constexpr int fit = 4 * 4 * slot <= LDS_PER_CU ? 4 : (4 * 3 * slot <= LDS_PER_CU ? 3 : 2);
+    return fit < MI_QMM_MAX_PIPE ? fit : MI_QMM_MAX_PIPE;
+}
+
+// s_waitcnt with vmcnt = N and no wait on the other counters (gfx9 encoding:
+// vmcnt[3:0] at bits 3:0 and vmcnt[5:4] at bits 15:14, expcnt 7, lgkmcnt 15).
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit count");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <typename T, int BITS, int A, int C, int WK, int PIPE, int EPI>
 __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
-    typedef MfmaShape<T, BITS, A, C, WK> Sh;
+    // The body uses gfx950 buffer resources, which the host target cannot
+    // type; the host pass needs only the launch stub.
+#if defined(__HIP_DEVICE_COMPILE__)
+    typedef MfmaShape<T, BITS, A, C, WK, PIPE> Sh;
     constexpr int P = epi_parts(EPI);
     static_assert(P == 1 || A == P, "multi-part epilogues use one tile per part");
     constexpr int TN = (P == 1) ? A : 1;  // 32-wide output tiles per wave
@@ -482,62 +559,102 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
     __shared__ __attribute__((aligned(16))) char lds[Sh::LDS];
 
     const int lane = threadIdx.x & 63;
-    const int kw = threadIdx.x >> 6;
+    // the wave index is uniform per wave: in a scalar register, the x stage
+    // base addresses and the DMA's LDS destinations (M0) need no VALU work
+    const int kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = lane >> 5, r = lane & 31;
     const int64_t K = p.K, G = K / p.gs;
-    const int64_t n_wave = select_part<EPI>(p, (int64_t)blockIdx.x * (32 * TN));
+    int64_t n_wave = (int64_t)blockIdx.x * (32 * TN);
+    const Bound bd = bind<EPI>(p, n_wave);
     const int64_t m_blk = (int64_t)blockIdx.y * (32 * C);
     const int wk = p.wk;
     const int Kw = (int)(K / wk);
     const int kbeg = kw * Kw;
     const int nst = Kw / XK;
-    char *xbuf = lds + kw * 2 * Sh::STAGE;
+    char *xbuf = lds + kw * PIPE * Sh::STAGE;
 
     // Rows past N (or tokens past M) read a clamped, valid row instead of
     // branching around the load: their accumulators only feed outputs the
-    // epilogue never stores, and branch-free loads keep the prefetch in flight.
-    const uint32_t *wrow[A];
-    const uint16_t *srow[A], *brow[A];
+    // epilogue never stores. All offsets are bytes within one array, under
+    // 2^32 (the host checks the sizes).
+    const int gshift = p.gs_log2;
+    __amdgpu_buffer_rsrc_t wr[A], sr[A], br[A];
+    uint32_t woff[A], sboff[A];
 #pragma unroll
     for (int a = 0; a < A; ++a) {
         const int part = (P == 1) ? 0 : a;
+        const int64_t rows = bd.noff(part) + bd.Nout;  // rows of this part's arrays
+        wr[a] = buffer_rsrc(bd.w(part), (uint32_t)(rows * K * BITS / 8));
+        sr[a] = buffer_rsrc(bd.s(part), (uint32_t)(rows * G * 2));
+        br[a] = buffer_rsrc(bd.b(part), (uint32_t)(rows * G * 2));
         const int64_t nout = n_wave + ((P == 1) ? 32 * a : 0) + r;
-        const int64_t row = p.noff[part] + (nout < p.Nout ? nout : p.Nout - 1);
-        wrow[a] = p.w[part] + row * (K / VPW) + 4 * h;
-        srow[a] = (const uint16_t *)p.s[part] + row * G;
-        brow[a] = (const uint16_t *)p.b[part] + row * G;
+        const int64_t row = bd.noff(part) + (nout < bd.Nout ? nout : bd.Nout - 1);
+        woff[a] = (uint32_t)(row * (K * BITS / 8) + 16 * h);
+        // group of value k0 + h * VPC for a super-step start k0 (a multiple of
+        // 2 * VPC): k0 / gs, plus h when a group is no wider than a half-chunk
+        const int hg = (p.gs <= VPC) ? h * (VPC >> gshift) : 0;
+        sboff[a] = (uint32_t)((row * G + hg) * 2);
     }
     // x DMA: instruction i writes stage rows 8i..8i+7; lane l fills row
     // 8i + l/8 at swizzled position l%8, i.e. it loads chunk (l%8) ^ swz(row).
-    const T *xbase = (const T *)p.x + kbeg;
-    int xoff[C * 4];
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(p.x, (uint32_t)(p.M * K * (int64_t)sizeof(T)));
+    uint32_t xoff[C * 4];
 #pragma unroll
     for (int i = 0; i < C * 4; ++i) {
         const int row = 8 * i + (lane >> 3);
         const int64_t m = m_blk + row < p.M ? m_blk + row : p.M - 1;
         const int chunk = (lane & 7) ^ ((row >> 1) & 7);
-        xoff[i] = (int)(m * K) + 8 * chunk;
+        xoff[i] = (uint32_t)((m * K + 8 * chunk) * (int64_t)sizeof(T));
     }
-    auto issue_x = [&](int st, int buf) {
-        char *dst = xbuf + buf * Sh::STAGE;
+    typedef __attribute__((address_space(3))) void *lds_ptr;
+    auto issue = [&](int st, char *slot) {
+        const int k0 = kbeg + st * XK;
+        const uint32_t xs = (uint32_t)k0 * sizeof(T);
 #pragma unroll
         for (int i = 0; i < C * 4; ++i)
-            __builtin_amdgcn_global_load_lds(
-                (const __attribute__((address_space(1))) void *)(xbase + xoff[i] + st * XK),
-                (__attribute__((address_space(3))) void *)(dst + i * 1024), 16, 0, 0);
-    };
-    const int gshift = p.gs_log2;
-    auto issue_w = [&](int st, uint4 (&wd)[A][SPS], uint32_t (&sd)[A][SPS],
-                       uint32_t (&bd)[A][SPS]) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(slot + i * 1024), 16, xoff[i],
+                                                     xs, 0, 0);
+        if constexpr (Sh::WREG) return;
 #pragma unroll
         for (int u = 0; u < SPS; ++u) {
-            const int k0 = kbeg + st * XK + u * SS;
-            const int g = (k0 + h * VPC) >> gshift;
+            const int ku = k0 + u * SS;
+            const uint32_t ws = (uint32_t)(ku / VPW) * 4;
+            const uint32_t gsoff = (uint32_t)(ku >> gshift) * 2;
 #pragma unroll
             for (int a = 0; a < A; ++a) {
-                wd[a][u] = ld16(wrow[a] + k0 / VPW);
-                sd[a][u] = srow[a][g];
-                bd[a][u] = brow[a][g];
+                char *wdst = slot + Sh::XST + (a * SPS + u) * 1024;
+                char *sdst = slot + Sh::XST + Sh::WST + (a * SPS + u) * 512;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wr[a], (lds_ptr)wdst, 16, woff[a], ws, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(sr[a], (lds_ptr)sdst, 2, sboff[a], gsoff,
+                                                         0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(br[a], (lds_ptr)(sdst + 256), 2, sboff[a],
+                                                         gsoff, 0, 0);
+            }
+        }
+    };
+    // WREG: the weight chunks, scales and biases of a stage into registers
+    uint4 wreg[2][A][SPS];
+    uint16_t sreg[2][A][SPS], breg[2][A][SPS];
+    const char *wlane[A], *slane[A], *blane[A];
+#pragma unroll
+    for (int a = 0; a < A; ++a) {
+        const int part = (P == 1) ? 0 : a;
+        wlane[a] = (const char *)bd.w(part) + woff[a];
+        slane[a] = (const char *)bd.s(part) + sboff[a];
+        blane[a] = (const char *)bd.b(part) + sboff[a];
+    }
+    auto load_w = [&](int st, uint4 (&wd)[A][SPS], uint16_t (&sd)[A][SPS],
+                      uint16_t (&bd_)[A][SPS]) {
+#pragma unroll
+        for (int u = 0; u < SPS; ++u) {
+            const int ku = kbeg + st * XK + u * SS;
+            const uint32_t ws = (uint32_t)(ku / VPW) * 4;
+            const uint32_t gsoff = (uint32_t)(ku >> gshift) * 2;
+#pragma unroll
+            for (int a = 0; a < A; ++a) {
+                wd[a][u] = ld16(wlane[a] + ws);
+                sd[a][u] = *(const uint16_t *)(slane[a] + gsoff);
+                bd_[a][u] = *(const uint16_t *)(blane[a] + gsoff);
             }
         }
     };
@@ -550,63 +667,94 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[a][c][i] = 0.0f;
 
-    // Pipeline: at the top of stage st every load issued during stage st-1
-    // (x DMA into buffer st&1, weights into wn_) has landed; the stage's x
-    // fragments are read out of LDS first, then the loads of stage st+1 are
-    // issued and overlap this stage's MFMAs.
-    uint4 wv[A][SPS], wn_[A][SPS];
-    uint32_t sv[A][SPS], bv[A][SPS], sn[A][SPS], bn[A][SPS];
-    if (nst > 0) {
-        issue_x(0, 0);
-        issue_w(0, wv, sv, bv);
-    }
+    // Pipeline, PIPE stages deep: while stage st computes, the DMAs of stage
+    // st + PIPE - 1 fill ring slot (st + PIPE - 1) % PIPE, which was last read
+    // by stage st - 1 (its ds_reads completed before its MFMAs). Every stage
+    // issues exactly OPS DMAs -- past the last stage they re-read stage
+    // nst - 1, in bounds, into slots no later stage reads -- so at the top of
+    // stage st at most the loads of the PIPE - 2 stages after it are in
+    // flight: vmcnt(VMCNT). The stage loop is unrolled PIPE times so each
+    // slot is named statically.
+    //
+    // The slots are passed as separate __restrict__ arguments of the inlined
+    // main loop: the resulting alias scopes let the compiler's wait-count
+    // pass see that a stage's ds_reads cannot touch the slots the DMAs in
+    // flight are filling, so it adds no vmcnt(0) of its own before them.
     const int swz = (r >> 1) & 7;
-    for (int st = 0; st < nst; ++st) {
-        const char *cur = xbuf + (st & 1) * Sh::STAGE;
-        // vmcnt(0): the x DMA and weight loads issued during stage st-1
-        __builtin_amdgcn_s_waitcnt(0x0F70);
-        uint4 xf[C][SPS][S];
+    auto mainloop = [&](char *__restrict__ b0, char *__restrict__ b1, char *__restrict__ b2,
+                        char *__restrict__ b3) __attribute__((always_inline)) {
+    auto ring = [&](int j) -> char * { return j == 0 ? b0 : (j == 1 ? b1 : (j == 2 ? b2 : b3)); };
+    const int last = nst > 0 ? nst - 1 : 0;
 #pragma unroll
-        for (int c = 0; c < C; ++c)
+    for (int j = 0; j < PIPE - 1; ++j) issue(j < last ? j : last, ring(j));
+    if constexpr (Sh::WREG) load_w(0, wreg[0], sreg[0], breg[0]);
+    for (int st0 = 0; st0 < nst; st0 += PIPE) {
+#pragma unroll
+        for (int j = 0; j < PIPE; ++j) {
+            const int st = st0 + j;
+            if (st >= nst) break;  // wave-uniform
+            wait_vmcnt<Sh::VMCNT>();
+            const char *cur = ring(j);
+            uint4 xf[C][SPS][S];
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+#pragma unroll
+                for (int u = 0; u < SPS; ++u)
+#pragma unroll
+                    for (int s = 0; s < S; ++s) {
+                        const int chunk = (u * SS + h * VPC + 8 * s) >> 3;
+                        xf[c][u][s] =
+                            *(const uint4 *)(cur + (32 * c + r) * 128 + ((chunk ^ swz) << 4));
+                    }
+            uint4 wq[A][SPS];
+            uint32_t sq[A][SPS], bq[A][SPS];
+#pragma unroll
+            for (int a = 0; a < A; ++a)
+#pragma unroll
+                for (int u = 0; u < SPS; ++u) {
+                    if constexpr (Sh::WREG) {
+                        wq[a][u] = wreg[j][a][u];
+                        sq[a][u] = sreg[j][a][u];
+                        bq[a][u] = breg[j][a][u];
+                    } else {
+                        wq[a][u] = *(const uint4 *)(cur + Sh::XST + (a * SPS + u) * 1024 + lane * 16);
+                        const char *sb = cur + Sh::XST + Sh::WST + (a * SPS + u) * 512;
+                        sq[a][u] = *(const uint32_t *)(sb + lane * 4);
+                        bq[a][u] = *(const uint32_t *)(sb + 256 + lane * 4);
+                    }
+                }
+            const int nx = st + PIPE - 1 < last ? st + PIPE - 1 : last;
+            issue(nx, ring((j + PIPE - 1) % PIPE));
+            if constexpr (Sh::WREG) {  // PIPE == 2: the next stage, into the other set
+                load_w(nx, wreg[(j + 1) % 2], sreg[(j + 1) % 2], breg[(j + 1) % 2]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int u = 0; u < SPS; ++u)
 #pragma unroll
-                for (int j = 0; j < S; ++j) {
-                    const int chunk = (u * SS + h * VPC + 8 * j) >> 3;
-                    xf[c][u][j] = *(const uint4 *)(cur + (32 * c + r) * 128 + ((chunk ^ swz) << 4));
-                }
-        const int nx = (st + 1 < nst) ? st + 1 : st;
-        if (st + 1 < nst) issue_x(nx, (st + 1) & 1);  // wave-uniform branch
-        issue_w(nx, wn_, sn, bn);
-        __builtin_amdgcn_sched_barrier(0);
+                for (int s = 0; s < S; ++s)
 #pragma unroll
-        for (int u = 0; u < SPS; ++u)
+                    for (int a = 0; a < A; ++a) {
+                        const uint32_t words[4] = {wq[a][u].x, wq[a][u].y, wq[a][u].z, wq[a][u].w};
+                        const float sf = (float)__builtin_bit_cast(T, (uint16_t)sq[a][u]);
+                        const float bf = (float)__builtin_bit_cast(T, (uint16_t)bq[a][u]);
+                        const V8 af = (BITS == 4)
+                                          ? dequant8<T, 4>(words[s], 0u, sf, bf)
+                                          : dequant8<T, 8>(words[2 * s], words[2 * s + 1], sf, bf);
 #pragma unroll
-            for (int j = 0; j < S; ++j)
-#pragma unroll
-                for (int a = 0; a < A; ++a) {
-                    const uint32_t words[4] = {wv[a][u].x, wv[a][u].y, wv[a][u].z, wv[a][u].w};
-                    const float sf = (float)__builtin_bit_cast(T, (uint16_t)sv[a][u]);
-                    const float bf = (float)__builtin_bit_cast(T, (uint16_t)bv[a][u]);
-                    const V8 af = (BITS == 4) ? dequant8<T, 4>(words[j], 0u, sf, bf)
-                                              : dequant8<T, 8>(words[2 * j], words[2 * j + 1], sf, bf);
-#pragma unroll
-                    for (int c = 0; c < C; ++c)
-                        acc[a][c] = Mfma<T>::mma(af, __builtin_bit_cast(V8, xf[c][u][j]), acc[a][c]);
-                }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int a = 0; a < A; ++a)
-#pragma unroll
-            for (int u = 0; u < SPS; ++u) {
-                wv[a][u] = wn_[a][u];
-                sv[a][u] = sn[a][u];
-                bv[a][u] = bn[a][u];
-                launder(wv[a][u]);
-                launder(sv[a][u]);
-                launder(bv[a][u]);
-            }
+                        for (int c = 0; c < C; ++c)
+                            acc[a][c] =
+                                Mfma<T>::mma(af, __builtin_bit_cast(V8, xf[c][u][s]), acc[a][c]);
+                    }
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
+    };
+    mainloop(xbuf, xbuf + (PIPE > 1 ? 1 : 0) * Sh::STAGE, xbuf + (PIPE > 2 ? 2 : 0) * Sh::STAGE,
+             xbuf + (PIPE > 3 ? 3 : 0) * Sh::STAGE);
+    // the loads issued past the last stage land before the LDS is reused for
+    // the reduction or released with the workgroup
+    wait_vmcnt<0>();
 
     if constexpr (WK > 1) {
         // fixed-order reduction of the K-split partial tiles; the LDS staging
@@ -651,7 +799,7 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
                     float v[1][4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) v[0][e] = acc[a][c][4 * blk + e];
-                    epi4<T, EPI, 1>(p, m, n_wave + 32 * a + 8 * blk + 4 * h, v);
+                    epi4<T, EPI, 1>(p, bd, m, n_wave + 32 * a + 8 * blk + 4 * h, v);
                 }
             } else {
                 float v[P][4];
@@ -659,10 +807,11 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
                 for (int q = 0; q < P; ++q)
 #pragma unroll
                     for (int e = 0; e < 4; ++e) v[q][e] = acc[q][c][4 * blk + e];
-                epi4<T, EPI, P>(p, m, n_wave + 8 * blk + 4 * h, v);
+                epi4<T, EPI, P>(p, bd, m, n_wave + 8 * blk + 4 * h, v);
             }
         }
     }
+#endif  // __HIP_DEVICE_COMPILE__
 }
 
 // ---------------------------------------------------------------------------
@@ -688,9 +837,10 @@ template <typename T, int BITS, int A, int C, int EPI>
 int launch_mfma_cfg(QParams p, int wk, hipStream_t st) {
     constexpr int P = epi_parts(EPI);
     constexpr int TN = (P == 1) ? A : 1;
+    constexpr int PIPE = mfma_pipe<T, BITS, A, C>();
     p.wk = wk;
     const dim3 grid((unsigned)ceil_div(p.Nout, 32 * TN), (unsigned)ceil_div(p.M, 32 * C));
-    qmm_mfma_kernel<T, BITS, A, C, 4, EPI><<<grid, 64 * wk, 0, st>>>(p);
+    qmm_mfma_kernel<T, BITS, A, C, 4, PIPE, EPI><<<grid, 64 * wk, 0, st>>>(p);
     return launch_status("quantized matmul (mfma)");
 }
 
@@ -710,7 +860,8 @@ int launch_mfma(const QParams &p, hipStream_t st) {
     const int64_t nt = ceil_div(p.Nout, 32);
     if constexpr (P == 1) {
         if (nt * ceil_div(p.M, 64) > 2048 && EPI != EPI_GROUP3)
-            return launch_mfma_cfg<T, BITS, 2, 4, EPI>(p, wk, st);
+            // (8-bit: 32x128, whose stage slots still fit the LDS twice)
+            return launch_mfma_cfg<T, BITS, BITS == 4 ? 2 : 1, 4, EPI>(p, wk, st);
     }
     if (p.M > 32 && nt * ceil_div(p.M, 64) >= 128)
         return launch_mfma_cfg<T, BITS, P, 2, EPI>(p, wk, st);
@@ -732,8 +883,11 @@ int launch_qmv_dot2(const QParams &p, int mr, hipStream_t st) {
 
 template <typename T, int EPI>
 int launch_typed(const QParams &p, int bits, hipStream_t st) {
+    // the MFMA kernel addresses x and each weight array with 32-bit offsets
+    const int64_t wrows = p.noff[2] + p.Nout;  // rows of the largest part's arrays
     const bool mfma = (sizeof(T) == 2) && p.M > QMV_MR && (p.K % XK == 0) &&
-                      p.M * p.K < ((int64_t)1 << 31);
+                      p.M * p.K < ((int64_t)1 << 31) &&
+                      wrows * p.K * bits / 8 < ((int64_t)1 << 32);
     if constexpr (sizeof(T) == 2) {
         const int mr = p.M == 1 ? 1 : (p.M == 2 ? 2 : 4);
         if (bits == 4 && p.M <= 4 && qmv_dot2_lds_bytes(mr, p.K) <= 65536)

@@ -169,7 +169,7 @@ def test_qmm_residual_rmsnorm(M):
     _close(y, oracle.rms_norm(to_np(h), nw, 1e-5, "bfloat16"), "bfloat16")
 
 
-@pytest.mark.parametrize("M", [1, 100])
+@pytest.mark.parametrize("M", [1, 100, 300])
 def test_qmm_split_gate(M):
     r = rng(600 + M)
     K, D = 1024, 256
@@ -182,7 +182,7 @@ def test_qmm_split_gate(M):
     _close(bx, bx_want, "bfloat16")
 
 
-@pytest.mark.parametrize("M", [1, 128])
+@pytest.mark.parametrize("M", [1, 20, 128, 300])
 def test_qmm_dual_and_swiglu(M):
     r = rng(700 + M)
     K, N = 1024, 384
@@ -362,6 +362,26 @@ def test_argmax_lowest_index_on_ties(dtype):
     assert got[0] == int(np.argmax(x[0]))
     assert got[1] == 77
     assert got[2] == 0
+
+
+@pytest.mark.parametrize("V", [1, 7, 1001, 8 * 1024 * 8 + 8, 65536])
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+def test_argmax_shapes_ties_nan_and_unaligned_rows(V, dtype):
+    """Vector (16-byte chunks) and scalar paths: random rows, a tie placed in
+    one thread's later chunk and another thread's earlier one, an all-NaN row
+    (-> 0), an all -inf row (-> 0), and a misaligned view (scalar path)."""
+    r = rng(1510 + V)
+    x = oracle.round_to(r.normal(0, 1, (5, V)), dtype)
+    if V > 16:
+        x[1, V - 3] = x[1, 9] = 40.0
+    x[2, :] = np.nan
+    x[3, :] = -np.inf
+    want = [int(np.argmax(x[0])), 9 if V > 16 else int(np.argmax(x[1])), 0, 0,
+            int(np.argmax(x[4]))]
+    got = ops.argmax(to_torch(x, dtype)).cpu().numpy()
+    assert got.tolist() == want
+    flat = to_torch(np.concatenate([[0.0], x[4]]).astype(np.float32), dtype)
+    assert int(ops.argmax(flat[1:].reshape(1, V)).item()) == want[4]  # data_ptr + 1 element
 
 
 def test_determinism_three_runs():
