@@ -149,6 +149,19 @@ int mi_norm_rope(const void *x, const void *w, void *out, int64_t B, int64_t L, 
                  float base, float scale, int64_t offset, int64_t out_seq_cap,
                  int64_t out_pos, int dtype, void *stream);
 
+/* The whole attention prologue in one launch (patch/wrappers.py:165-176):
+ * q [B, L, Hq, D] (row stride q_row_stride) -> rms_norm(q_norm) -> rope ->
+ * q_out [B, Hq, L, D]; k [B, L, Hkv, D] -> rms_norm(k_norm) -> rope -> written
+ * into k_cache [B, Hkv, kv_cap, D] at rows [kv_pos, kv_pos + L); v -> copied
+ * (transposed) into v_cache likewise -- the cache's update_and_fetch. Each
+ * output equals the corresponding mi_norm_rope call bit for bit. */
+int mi_norm_rope_qkv(const void *q, const void *k, const void *v, int64_t q_row_stride,
+                     int64_t k_row_stride, int64_t v_row_stride, const void *q_norm,
+                     const void *k_norm, void *q_out, void *k_cache, void *v_cache, int64_t B,
+                     int64_t L, int64_t Hq, int64_t Hkv, int64_t D, float eps, int rope_dims,
+                     int traditional, float base, float scale, int64_t offset, int64_t kv_cap,
+                     int64_t kv_pos, int dtype, void *stream);
+
 /* mx.fast.scaled_dot_product_attention(q, k, v, scale, mask='causal'|None):
  * q [B, H, Lq, D]; k, v [B, HK, kv_cap, D] of which rows [0, Lk) are valid;
  * kv head of q head h is h / (H / HK); causal is bottom-right aligned (query

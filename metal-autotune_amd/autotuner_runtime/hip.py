@@ -49,6 +49,8 @@ SIGNATURES: dict[str, list] = {
     "mi_rms_norm": [_P, _P, _P, _I64, _I64, _F, _I, _P],
     "mi_norm_rope": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _F, _F, _I64, _I64,
                      _I64, _I, _P],
+    "mi_norm_rope_qkv": [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64,
+                         _I64, _I64, _F, _I, _I, _F, _F, _I64, _I64, _I64, _I, _P],
     "mi_sdpa": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _I, _P],
     "mi_swiglu": [_P, _P, _P, _I64, _I, _P],
     "mi_shortconv": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P],

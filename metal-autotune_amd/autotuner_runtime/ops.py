@@ -140,6 +140,39 @@ def norm_rope(x, weight, n_heads: int, eps: float, dims: int, base: float, offse
     return out
 
 
+def norm_rope_qkv(q, k, v, q_norm, k_norm, n_heads: int, n_kv_heads: int, eps: float, dims: int,
+                  base: float, offset: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                  cache_pos: int, traditional: bool = False, scale: float = 1.0) -> torch.Tensor:
+    """The attention prologue in one launch: q -> rms_norm -> rope -> [B, H, L, D]
+    (returned); k -> rms_norm -> rope and v -> transpose, written into the
+    caches at rows [cache_pos, cache_pos + L). Equal bit for bit to three
+    norm_rope calls. q, k, v may be row-strided views ([B, L, H*D] slices)."""
+    B, L, _ = q.shape
+    D = q.shape[-1] // n_heads
+    for t, h in ((k, n_kv_heads), (v, n_kv_heads)):
+        if t.shape[:2] != (B, L) or t.shape[-1] != h * D or t.dtype != q.dtype:
+            raise ValueError("q, k and v must share batch, length, head dim and dtype")
+    for t in (q, k, v):
+        if t.stride(-1) != 1 or t.stride(0) != L * t.stride(1):
+            raise ValueError("q, k, v rows must be unit-stride with a uniform row stride")
+    for c in (k_cache, v_cache):
+        if (not c.is_contiguous() or c.shape[0] != B or c.shape[1] != n_kv_heads
+                or c.shape[3] != D or c.dtype != q.dtype):
+            raise ValueError(f"cache {tuple(c.shape)} does not hold {(B, n_kv_heads, '*', D)}")
+    for wt in (q_norm, k_norm):
+        if tuple(wt.shape) != (D,) or wt.dtype != q.dtype:
+            raise ValueError(f"norm weight must be {q.dtype} [{D}]")
+    out = _empty((B, n_heads, L, D), q)
+    hip._require_gpu(q)
+    hip._check(hip.lib().mi_norm_rope_qkv(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(1), k.stride(1), v.stride(1),
+        q_norm.data_ptr(), k_norm.data_ptr(), out.data_ptr(), k_cache.data_ptr(),
+        v_cache.data_ptr(), B, L, n_heads, n_kv_heads, D, float(eps), int(dims),
+        int(traditional), float(base), float(scale), int(offset), k_cache.shape[2],
+        int(cache_pos), hip._dt(q), hip._stream(q)), "norm_rope_qkv")
+    return out
+
+
 def rope(x, dims: int, traditional: bool = False, base: float = 10000.0, scale: float = 1.0,
          offset: int = 0) -> torch.Tensor:
     """mx.fast.rope on [..., L, D] (the position axis is -2)."""

@@ -91,17 +91,37 @@ __global__ __launch_bounds__(256) void attn_kernel(const T *__restrict__ q,
     const T *kb = k + (b * HK + hk) * cap * D;
     const T *vb = v + (b * HK + hk) * cap * D;
 
-    for (int kt = 0; kt < ntiles; ++kt) {
-        __syncthreads();
-        for (int c = threadIdx.x; c < KT * D / 8; c += 256) {
+    // K/V tile staging: each thread owns CH 16-byte chunks of a tile. The
+    // chunks of tile kt + 1 are loaded into registers while tile kt computes,
+    // so a tile's global-load latency overlaps the previous tile's MFMAs.
+    constexpr int CH = KT * D / 8 / 256;
+    uint4 kreg[CH], vreg[CH];
+    auto fetch = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int c = threadIdx.x + 256 * i;
             const int key = c / (D / 8), dc = c % (D / 8);
             const int64_t kg = (int64_t)kt * KT + key;
-            const bool ok = kg < Lk;
-            *(uint4 *)(ks + key * KP + dc * 8) = ok ? ld16(kb + kg * D + dc * 8) : make_uint4(0, 0, 0, 0);
-            const V8 vv = __builtin_bit_cast(V8, ok ? ld16(vb + kg * D + dc * 8) : make_uint4(0, 0, 0, 0));
+            const int64_t kc = kg < Lk ? kg : Lk - 1;  // in bounds; masked below
+            kreg[i] = ld16(kb + kc * D + dc * 8);
+            vreg[i] = ld16(vb + kc * D + dc * 8);
+        }
+    };
+    if (ntiles > 0) fetch(0);
+
+    for (int kt = 0; kt < ntiles; ++kt) {
+        __syncthreads();  // every wave is done with tile kt - 1
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int c = threadIdx.x + 256 * i;
+            const int key = c / (D / 8), dc = c % (D / 8);
+            const bool ok = (int64_t)kt * KT + key < Lk;
+            *(uint4 *)(ks + key * KP + dc * 8) = ok ? kreg[i] : make_uint4(0, 0, 0, 0);
+            const V8 vv = __builtin_bit_cast(V8, ok ? vreg[i] : make_uint4(0, 0, 0, 0));
 #pragma unroll
             for (int e = 0; e < 8; ++e) vts[(dc * 8 + e) * VP + key] = vv[e];
         }
+        if (kt + 1 < ntiles) fetch(kt + 1);  // workgroup-uniform
         __syncthreads();
         if (!active) continue;
 

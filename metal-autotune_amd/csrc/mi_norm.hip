@@ -64,11 +64,69 @@ __global__ __launch_bounds__(256) void rms_kernel(const T *__restrict__ x, const
     }
 }
 
+// Wide rows (16-bit T, D % 8 == 0, D <= 8 * 256 * RC): one 256-thread
+// workgroup per row, the row held in registers between the sum of squares and
+// the scaled store, so x is read once and every load is issued up front.
+// Same arithmetic as rms_kernel: fma sum of squares in chunk order per
+// thread, then a fixed-order reduction (xor tree in each wave, waves 0..3).
+constexpr int RMS_RC = 2;  // 16-byte chunks per thread
+
+template <typename T>
+__global__ __launch_bounds__(256) void rms_row_kernel(const T *__restrict__ x,
+                                                      const T *__restrict__ w, T *__restrict__ y,
+                                                      int64_t D, float eps) {
+    __shared__ float part[4];
+    const int64_t row = blockIdx.x;
+    const T *xr = x + row * D;
+    T *yr = y + row * D;
+    const int nc = (int)(D / 8);
+    uint4 xv[RMS_RC];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RMS_RC; ++i) {
+        const int c = threadIdx.x + 256 * i;
+        xv[i] = ld16(xr + 8 * (c < nc ? c : nc - 1));  // clamped: in bounds, unused past nc
+    }
+#pragma unroll
+    for (int i = 0; i < RMS_RC; ++i) {
+        if (threadIdx.x + 256 * i < nc) {
+            float f[8];
+            unpack8<T>(xv[i], f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(f[e], f[e], ss);
+        }
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = ((part[0] + part[1]) + part[2]) + part[3];
+    const float inv = 1.0f / __fsqrt_rn(ss / (float)D + eps);
+#pragma unroll
+    for (int i = 0; i < RMS_RC; ++i) {
+        const int c = threadIdx.x + 256 * i;
+        if (c < nc) {
+            float f[8], g[8];
+            unpack8<T>(xv[i], f);
+            unpack8<T>(ld16(w + 8 * c), g);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = g[e] * (float)cvt<T>(f[e] * inv);
+            st16(yr + 8 * c, pack8<T>(f));
+        }
+    }
+}
+
 template <typename T>
 int launch_rms(const void *x, const void *w, void *y, int64_t rows, int64_t D, float eps,
                hipStream_t st) {
     if (rows == 0) return MI_OK;
     const int vec = D % 8 == 0 && aligned(x, 16) && aligned(w, 16) && aligned(y, 16);
+    if constexpr (sizeof(T) == 2) {
+        if (vec && D >= 1024 && D <= 8 * 256 * RMS_RC) {
+            rms_row_kernel<T><<<(unsigned)rows, 256, 0, st>>>((const T *)x, (const T *)w,
+                                                              (T *)y, D, eps);
+            return launch_status("rms_norm");
+        }
+    }
     rms_kernel<T><<<(unsigned)ceil_div(rows, 4), 256, 0, st>>>((const T *)x, (const T *)w,
                                                                 (T *)y, rows, D, eps, vec);
     return launch_status("rms_norm");
@@ -76,14 +134,40 @@ int launch_rms(const void *x, const void *w, void *y, int64_t rows, int64_t D, f
 
 // One row = one head vector of D values, owned by R lanes (R a power of two).
 // Slot p < dims/2 is a rotated pair; slots past it copy two tail values.
+// One launch serves up to three jobs (the attention prologue's q, k and v):
+// each job has its own input (row stride xs), norm weight (NULL: no norm),
+// head count, output [B, H, cap, D] at rows pos0.., and rope dims (0: none).
+// Rows are numbered job 0 first, then 1, then 2.
+struct NRJob {
+    const void *x, *w;
+    void *out;
+    int64_t H, xs, cap, pos0;
+    int dims;
+};
+struct NRJobs {
+    NRJob j0, j1, j2;
+    int64_t end0, end1, rows;  // cumulative row ends
+};
+
 template <typename T, int R>
-__global__ __launch_bounds__(256) void norm_rope_kernel(
-    const T *__restrict__ x, const T *__restrict__ w, T *__restrict__ out, int64_t B, int64_t L,
-    int64_t H, int64_t D, int64_t xs, float eps, int dims, int trad, float log2base,
-    float scale, int64_t offset, int64_t cap, int64_t pos0) {
+__global__ __launch_bounds__(256) void norm_rope_kernel(NRJobs jobs, int64_t B, int64_t L,
+                                                        int64_t D, float eps, int trad,
+                                                        float log2base, float scale,
+                                                        int64_t offset) {
     const int t = threadIdx.x % R;
-    const int64_t row = (int64_t)blockIdx.x * (256 / R) + threadIdx.x / R;
-    if (row >= B * L * H) return;
+    int64_t row = (int64_t)blockIdx.x * (256 / R) + threadIdx.x / R;
+    if (row >= jobs.rows) return;
+    // the row's job, selected field by field (no indexed copy of the table)
+    const bool a0 = row < jobs.end0, a1 = !a0 && row < jobs.end1;
+    row -= a0 ? 0 : (a1 ? jobs.end0 : jobs.end1);
+    const T *x = (const T *)(a0 ? jobs.j0.x : (a1 ? jobs.j1.x : jobs.j2.x));
+    const T *w = (const T *)(a0 ? jobs.j0.w : (a1 ? jobs.j1.w : jobs.j2.w));
+    T *out = (T *)(a0 ? jobs.j0.out : (a1 ? jobs.j1.out : jobs.j2.out));
+    const int64_t H = a0 ? jobs.j0.H : (a1 ? jobs.j1.H : jobs.j2.H);
+    const int64_t xs = a0 ? jobs.j0.xs : (a1 ? jobs.j1.xs : jobs.j2.xs);
+    const int64_t cap = a0 ? jobs.j0.cap : (a1 ? jobs.j1.cap : jobs.j2.cap);
+    const int64_t pos0 = a0 ? jobs.j0.pos0 : (a1 ? jobs.j1.pos0 : jobs.j2.pos0);
+    const int dims = a0 ? jobs.j0.dims : (a1 ? jobs.j1.dims : jobs.j2.dims);
     const int64_t h = row % H, l = (row / H) % L, b = row / (H * L);
     const T *xr = x + (b * L + l) * xs + h * D;
     T *orow = out + ((b * H + h) * cap + pos0 + l) * D;
@@ -131,16 +215,14 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(
 }
 
 template <typename T>
-int launch_norm_rope(const void *x, const void *w, void *out, int64_t B, int64_t L, int64_t H,
-                     int64_t D, int64_t xs, float eps, int dims, int trad, float log2base,
-                     float scale, int64_t offset, int64_t cap, int64_t pos0, hipStream_t st) {
-    const int64_t rows = B * L * H;
+int launch_norm_rope(const NRJobs &jobs, int64_t B, int64_t L, int64_t D, float eps, int trad,
+                     float log2base, float scale, int64_t offset, hipStream_t st) {
+    const int64_t rows = jobs.rows;
     if (rows == 0) return MI_OK;
     const int64_t slots = D / 2;
 #define MI_NR_LAUNCH(RR)                                                                       \
     norm_rope_kernel<T, RR><<<(unsigned)ceil_div(rows, 256 / RR), 256, 0, st>>>(                \
-        (const T *)x, (const T *)w, (T *)out, B, L, H, D, xs, eps, dims, trad, log2base, scale, \
-        offset, cap, pos0)
+        jobs, B, L, D, eps, trad, log2base, scale, offset)
     if (slots >= 64)
         MI_NR_LAUNCH(64);
     else if (slots >= 32)
@@ -192,36 +274,87 @@ extern "C" int mi_qmm_affine_residual_rmsnorm(const void *x, const uint32_t *w,
     return rms_launch(h, norm_w, y, M, N, eps, dtype, stream);
 }
 
+namespace mi {
+namespace {
+
+// Checks one job and appends it to the table (rows numbered in job order).
+int add_job(NRJobs &jobs, int n, const void *x, const void *w, void *out, int64_t B, int64_t L,
+            int64_t H, int64_t D, int64_t xs, int dims, int64_t cap, int64_t pos) {
+    if (B < 0 || L < 0 || H <= 0 || D <= 0 || D % 2)
+        return fail(MI_ERR_ARG, "norm_rope shape B=%lld L=%lld H=%lld D=%lld", (long long)B,
+                    (long long)L, (long long)H, (long long)D);
+    if (dims < 0 || dims > D || dims % 2)
+        return fail(MI_ERR_ARG, "rope dims %d vs head dim %lld", dims, (long long)D);
+    if (xs < H * D) return fail(MI_ERR_ARG, "x row stride smaller than H*D");
+    if (pos < 0 || pos + L > cap)
+        return fail(MI_ERR_ARG, "rows [%lld, %lld) exceed the output capacity %lld",
+                    (long long)pos, (long long)(pos + L), (long long)cap);
+    if (B * L && (!x || !out)) return fail(MI_ERR_ARG, "null pointer");
+    const NRJob j = {x, w, out, H, xs, cap, pos, dims};
+    const int64_t start = jobs.rows;
+    jobs.rows += B * L * H;
+    if (n == 0) {
+        jobs.j0 = jobs.j1 = jobs.j2 = j;
+        jobs.end0 = jobs.end1 = jobs.rows;
+    } else if (n == 1) {
+        jobs.j1 = jobs.j2 = j;
+        jobs.end0 = start;
+        jobs.end1 = jobs.rows;
+    } else {
+        jobs.j2 = j;
+        jobs.end1 = start;
+    }
+    return MI_OK;
+}
+
+int run_norm_rope(const NRJobs &jobs, int64_t B, int64_t L, int64_t D, float eps, int dims,
+                  int trad, float base, float scale, int64_t offset, int dtype, void *stream) {
+    if (dims && !(base > 0.0f)) return fail(MI_ERR_ARG, "rope base must be positive");
+    const float log2base = dims ? (float)log2((double)base) : 0.0f;
+    hipStream_t st = as_stream(stream);
+    switch (dtype) {
+    case MI_BF16:
+        return launch_norm_rope<bf16>(jobs, B, L, D, eps, trad, log2base, scale, offset, st);
+    case MI_F16:
+        return launch_norm_rope<f16>(jobs, B, L, D, eps, trad, log2base, scale, offset, st);
+    default:
+        return launch_norm_rope<float>(jobs, B, L, D, eps, trad, log2base, scale, offset, st);
+    }
+}
+
+}  // namespace
+}  // namespace mi
+
 extern "C" int mi_norm_rope(const void *x, const void *w, void *out, int64_t B, int64_t L,
                             int64_t H, int64_t D, int64_t x_row_stride, float eps, int rope_dims,
                             int traditional, float base, float scale, int64_t offset,
                             int64_t out_seq_cap, int64_t out_pos, int dtype, void *stream) {
     if (!valid_dtype(dtype)) return fail(MI_ERR_UNSUPPORTED, "dtype code %d", dtype);
-    if (B < 0 || L < 0 || H <= 0 || D <= 0 || D % 2)
-        return fail(MI_ERR_ARG, "norm_rope shape B=%lld L=%lld H=%lld D=%lld", (long long)B,
-                    (long long)L, (long long)H, (long long)D);
-    if (rope_dims < 0 || rope_dims > D || rope_dims % 2)
-        return fail(MI_ERR_ARG, "rope dims %d vs head dim %lld", rope_dims, (long long)D);
-    if (x_row_stride < H * D) return fail(MI_ERR_ARG, "x row stride smaller than H*D");
-    if (out_pos < 0 || out_pos + L > out_seq_cap)
-        return fail(MI_ERR_ARG, "rows [%lld, %lld) exceed the output capacity %lld",
-                    (long long)out_pos, (long long)(out_pos + L), (long long)out_seq_cap);
-    if (rope_dims && !(base > 0.0f)) return fail(MI_ERR_ARG, "rope base must be positive");
-    if (B * L && (!x || !out)) return fail(MI_ERR_ARG, "null pointer");
-    const float log2base = rope_dims ? (float)log2((double)base) : 0.0f;
-    hipStream_t st = as_stream(stream);
-    switch (dtype) {
-    case MI_BF16:
-        return launch_norm_rope<bf16>(x, w, out, B, L, H, D, x_row_stride, eps, rope_dims,
-                                      traditional, log2base, scale, offset, out_seq_cap, out_pos,
-                                      st);
-    case MI_F16:
-        return launch_norm_rope<f16>(x, w, out, B, L, H, D, x_row_stride, eps, rope_dims,
-                                     traditional, log2base, scale, offset, out_seq_cap, out_pos,
-                                     st);
-    default:
-        return launch_norm_rope<float>(x, w, out, B, L, H, D, x_row_stride, eps, rope_dims,
-                                       traditional, log2base, scale, offset, out_seq_cap, out_pos,
-                                       st);
-    }
+    NRJobs jobs = {};
+    if (int e = add_job(jobs, 0, x, w, out, B, L, H, D, x_row_stride, rope_dims, out_seq_cap,
+                        out_pos))
+        return e;
+    return run_norm_rope(jobs, B, L, D, eps, rope_dims, traditional, base, scale, offset, dtype,
+                         stream);
+}
+
+extern "C" int mi_norm_rope_qkv(const void *q, const void *k, const void *v, int64_t q_row_stride,
+                                int64_t k_row_stride, int64_t v_row_stride, const void *q_norm,
+                                const void *k_norm, void *q_out, void *k_cache, void *v_cache,
+                                int64_t B, int64_t L, int64_t Hq, int64_t Hkv, int64_t D,
+                                float eps, int rope_dims, int traditional, float base,
+                                float scale, int64_t offset, int64_t kv_cap, int64_t kv_pos,
+                                int dtype, void *stream) {
+    if (!valid_dtype(dtype)) return fail(MI_ERR_UNSUPPORTED, "dtype code %d", dtype);
+    NRJobs jobs = {};
+    if (int e = add_job(jobs, 0, q, q_norm, q_out, B, L, Hq, D, q_row_stride, rope_dims, L, 0))
+        return e;
+    if (int e = add_job(jobs, 1, k, k_norm, k_cache, B, L, Hkv, D, k_row_stride, rope_dims,
+                        kv_cap, kv_pos))
+        return e;
+    if (int e = add_job(jobs, 2, v, nullptr, v_cache, B, L, Hkv, D, v_row_stride, 0, kv_cap,
+                        kv_pos))
+        return e;
+    return run_norm_rope(jobs, B, L, D, eps, rope_dims, traditional, base, scale, offset, dtype,
+                         stream);
 }

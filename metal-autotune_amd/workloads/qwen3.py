@@ -210,11 +210,11 @@ class Qwen3LayerRegions(ReplayWrapper):
         outs = _kernels.try_sized(self._specs["qkv"],
                                   [xn] + [t for m in projs for t in (m.weight, m.scales, m.biases)])
         q, k, v = (m(xn) for m in projs) if outs is None else outs
-        qr = ops.norm_rope(q, attn.q_norm.weight, c.num_attention_heads, c.rms_norm_eps,
-                           c.head_dim, c.rope_theta, cache.offset)
-        ops.norm_rope(k, attn.k_norm.weight, c.num_key_value_heads, c.rms_norm_eps, c.head_dim,
-                      c.rope_theta, cache.offset, out=cache.keys, out_pos=cache.offset)
-        ops.write_kv(v, c.num_key_value_heads, cache.values, cache.offset)
+        # q/k-norm + RoPE + the KV-cache update, one launch
+        qr = ops.norm_rope_qkv(q, k, v, attn.q_norm.weight, attn.k_norm.weight,
+                               c.num_attention_heads, c.num_key_value_heads, c.rms_norm_eps,
+                               c.head_dim, c.rope_theta, cache.offset, cache.keys, cache.values,
+                               cache.offset)
         o = ops.scaled_dot_product_attention(qr, cache.keys, cache.values, attn.scale,
                                              "causal" if L > 1 else None,
                                              kv_len=cache.offset + L,

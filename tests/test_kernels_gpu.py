@@ -281,6 +281,37 @@ def test_norm_rope_into_cache():
     assert (c[:, :, :10] == 7.0).all() and (c[:, :, 15:] == 7.0).all()
 
 
+@pytest.mark.parametrize("L,offset,strided", [(128, 0, False), (1, 128, False), (7, 3, True)])
+def test_norm_rope_qkv_equals_three_calls(L, offset, strided):
+    """The one-launch attention prologue == q norm_rope + k norm_rope into the
+    cache + v cache write, bit for bit; q/k/v may be column slices of one
+    [B, L, (H + 2 HK) D] buffer (row stride > H D); cache rows outside
+    [offset, offset + L) stay untouched."""
+    r = rng(970 + L)
+    H, HK, D, cap = 32, 8, 128, 160
+    qkv = oracle.round_to(r.normal(0, 1, (1, L, (H + 2 * HK) * D)), "bfloat16")
+    qn = oracle.round_to(1 + 0.2 * r.normal(0, 1, D), "bfloat16")
+    kn = oracle.round_to(1 + 0.2 * r.normal(0, 1, D), "bfloat16")
+    t = to_torch(qkv, "bfloat16")
+    if strided:
+        q, k, v = t[..., :H * D], t[..., H * D:(H + HK) * D], t[..., (H + HK) * D:]
+    else:
+        q, k, v = (t[..., :H * D].contiguous(), t[..., H * D:(H + HK) * D].contiguous(),
+                   t[..., (H + HK) * D:].contiguous())
+    qw, kw = to_torch(qn, "bfloat16"), to_torch(kn, "bfloat16")
+    kc = torch.full((1, HK, cap, D), 5.0, dtype=torch.bfloat16, device="cuda")
+    vc = torch.full_like(kc, 6.0)
+    qr = ops.norm_rope_qkv(q, k, v, qw, kw, H, HK, 1e-6, D, 1e6, offset, kc, vc, offset)
+    kc2, vc2 = torch.full_like(kc, 5.0), torch.full_like(kc, 6.0)
+    qr2 = ops.norm_rope(q.contiguous(), qw, H, 1e-6, D, 1e6, offset)
+    ops.norm_rope(k.contiguous(), kw, HK, 1e-6, D, 1e6, offset, out=kc2, out_pos=offset)
+    ops.write_kv(v.contiguous(), HK, vc2, offset)
+    assert torch.equal(qr, qr2) and torch.equal(kc, kc2) and torch.equal(vc, vc2)
+    _close(qr, oracle.norm_rope(qkv[..., :H * D], qn, 1e-6, H, D, 1e6, offset, "bfloat16"),
+           "bfloat16")
+    assert (to_np(kc)[:, :, offset + L:] == 5.0).all() and (to_np(vc)[:, :, :offset] == 6.0).all()
+
+
 @pytest.mark.parametrize("H,HK,Lq,Lk,D,causal", [(32, 8, 128, 128, 128, True),
                                                  (32, 8, 1, 129, 128, True),
                                                  (32, 8, 200, 200, 64, True),
