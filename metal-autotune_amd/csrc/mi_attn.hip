@@ -94,13 +94,16 @@ __global__ __launch_bounds__(256) void attn_kernel(const T *__restrict__ q,
     // K/V tile staging: each thread owns CH 16-byte chunks of a tile. The
     // chunks of tile kt + 1 are loaded into registers while tile kt computes,
     // so a tile's global-load latency overlaps the previous tile's MFMAs.
+    // Consecutive lanes take consecutive keys: the transposed V stores of a
+    // wave then hit consecutive 2-byte LDS addresses (with the head-dim chunk
+    // fastest, 16 lanes would store into one bank).
     constexpr int CH = KT * D / 8 / 256;
     uint4 kreg[CH], vreg[CH];
     auto fetch = [&](int kt) {
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
             const int c = threadIdx.x + 256 * i;
-            const int key = c / (D / 8), dc = c % (D / 8);
+            const int key = c % KT, dc = c / KT;
             const int64_t kg = (int64_t)kt * KT + key;
             const int64_t kc = kg < Lk ? kg : Lk - 1;  // in bounds; masked below
             kreg[i] = ld16(kb + kc * D + dc * 8);
@@ -114,7 +117,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const T *__restrict__ q,
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
             const int c = threadIdx.x + 256 * i;
-            const int key = c / (D / 8), dc = c % (D / 8);
+            const int key = c % KT, dc = c / KT;
             const bool ok = (int64_t)kt * KT + key < Lk;
             *(uint4 *)(ks + key * KP + dc * 8) = ok ? kreg[i] : make_uint4(0, 0, 0, 0);
             const V8 vv = __builtin_bit_cast(V8, ok ? vreg[i] : make_uint4(0, 0, 0, 0));

@@ -346,6 +346,27 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
         br[q] = (const T *)bd.b(q) + row * G;
     }
 
+    // The first batch of weight chunks is requested before x is staged, so the
+    // two memory round trips overlap (for K up to 16 lanes x QV_BATCH x 32
+    // values, that batch is the whole row).
+    uint4 wv[P][QV_BATCH];
+    T sv[P][QV_BATCH], bv[P][QV_BATCH];
+    auto load_batch = [&](int64_t base) {
+#pragma unroll
+        for (int i = 0; i < QV_BATCH; ++i) {
+            const int64_t c = base + 16 * i;
+            const int64_t cc = c < cpr ? c : cpr - 1;
+            const int64_t g = (cc * 32) >> p.gs_log2;
+#pragma unroll
+            for (int q = 0; q < P; ++q) {
+                wv[q][i] = ld16(wr[q] + 4 * cc);
+                sv[q][i] = sr[q][g];
+                bv[q][i] = br[q][g];
+            }
+        }
+    };
+    load_batch(j);
+
     // stage x rows as pairs (e[i], e[i+4]) of each 8-value block
     const T *x = (const T *)p.x + m0 * K;
     for (int64_t idx = threadIdx.x; idx < MR * words; idx += 256) {
@@ -379,20 +400,7 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
         for (int m = 0; m < MR; ++m) acc[q][m] = 0.0f;
 
     for (int64_t base = j; base < cpr; base += 16 * QV_BATCH) {
-        uint4 wv[P][QV_BATCH];
-        T sv[P][QV_BATCH], bv[P][QV_BATCH];
-#pragma unroll
-        for (int i = 0; i < QV_BATCH; ++i) {
-            const int64_t c = base + 16 * i;
-            const int64_t cc = c < cpr ? c : cpr - 1;
-            const int64_t g = (cc * 32) >> p.gs_log2;
-#pragma unroll
-            for (int q = 0; q < P; ++q) {
-                wv[q][i] = ld16(wr[q] + 4 * cc);
-                sv[q][i] = sr[q][g];
-                bv[q][i] = br[q][g];
-            }
-        }
+        if (base != j) load_batch(base);  // the first batch is already in flight
 #pragma unroll
         for (int i = 0; i < QV_BATCH; ++i) {
             const int64_t c = base + 16 * i;
