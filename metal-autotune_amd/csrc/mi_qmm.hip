@@ -346,9 +346,9 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
         br[q] = (const T *)bd.b(q) + row * G;
     }
 
-    // The first batch of weight chunks is requested before x is staged, so the
-    // two memory round trips overlap (for K up to 16 lanes x QV_BATCH x 32
-    // values, that batch is the whole row).
+    // (Requesting the first weight batch before x is staged was measured: it
+    // holds the batch registers through the staging, and the lost occupancy
+    // cost more at N = 151936 than the overlap gained at N = 9728.)
     uint4 wv[P][QV_BATCH];
     T sv[P][QV_BATCH], bv[P][QV_BATCH];
     auto load_batch = [&](int64_t base) {
@@ -365,7 +365,6 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
             }
         }
     };
-    load_batch(j);
 
     // stage x rows as pairs (e[i], e[i+4]) of each 8-value block
     const T *x = (const T *)p.x + m0 * K;
@@ -400,7 +399,7 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
         for (int m = 0; m < MR; ++m) acc[q][m] = 0.0f;
 
     for (int64_t base = j; base < cpr; base += 16 * QV_BATCH) {
-        if (base != j) load_batch(base);  // the first batch is already in flight
+        load_batch(base);
 #pragma unroll
         for (int i = 0; i < QV_BATCH; ++i) {
             const int64_t c = base + 16 * i;
