@@ -55,6 +55,7 @@ struct QParams {
     int gs;
     int gs_log2;               // log2(gs): group sizes are powers of two
     int wk;                    // K-split waves (qmm_mfma_kernel)
+    int sbp;                   // qmm_mfma_kernel: groups per row of a wave's scale/bias table
 };
 
 template <typename T> __device__ __forceinline__ float swiglu1(float g, float u) {
@@ -471,20 +472,27 @@ template <> struct Mfma<f16> {
 };
 
 // A: 32-row weight tiles per wave (one per part when P > 1); C: 32-token
-// tiles per wave; WK: waves per workgroup, each owning a 1/wk slice of K.
+// tiles per wave; WK: waves per workgroup; WF: waves that share one x stage
+// and each own a different 32 * A-feature tile. The workgroup's waves form
+// wk = (waves / WF) K-groups, each owning a 1/wk slice of K.
 //
-// Everything a stage needs reaches the wave through LDS by direct-to-LDS DMA
-// (buffer_load ... lds), into a ring of PIPE stage slots per wave:
+// Everything a stage needs reaches the waves through LDS by direct-to-LDS DMA
+// (buffer_load ... lds), into a ring of PIPE stage slots per K-group:
 //  * the x tile of the stage, 8 token rows x 128 bytes per instruction, so
 //    every x cache line is fetched once (loading x fragments straight into
 //    registers makes each lane read a different token row, and with four
-//    waves the per-step working set overflows the 32 KB L1). The 16-byte
+//    waves the per-step working set overflows the 32 KB L1). The WF waves of
+//    a K-group issue 1/WF of those instructions each and meet at a barrier
+//    before reading the tile. The 16-byte
 //    chunks of a row are XOR-swizzled by (row >> 1) & 7 so a 16-lane
 //    ds_read_b128 group covers 16 distinct bank groups;
 //  * each lane's 16-byte weight chunk, per part and super-step (lane l's
-//    chunk lands at l * 16, where the same lane reads it back);
-//  * each lane's scale and bias (2-byte DMA writes one zero-extended dword
-//    per lane, at l * 4).
+//    chunk lands at l * 16, where the same lane reads it back).
+// The scales and biases of a wave's rows over its whole K slice are copied
+// once, before the loop, into a per-wave table in dynamic LDS (sbt_layout):
+// per-stage 2-byte loads touch one cache line per row for two bytes each,
+// and measured on MI355X those gathers cost more load-pipeline time than the
+// weights themselves.
 // With no load result held in registers across stages, the explicit vmcnt
 // at the top of a stage is the only wait the loop needs, and the addresses
 // are a per-lane 32-bit offset plus a scalar stage offset (no VALU address
@@ -492,7 +500,9 @@ template <> struct Mfma<f16> {
 constexpr int XK = 64;  // k values per x stage (128 bytes of a token row)
 constexpr int LDS_PER_CU = 160 * 1024;
 
-template <typename T, int BITS, int A, int C, int WK, int PIPE>
+constexpr int MAX_PIPE = 8;  // ring slots per K-group at most
+
+template <typename T, int BITS, int A, int C, int WK, int PIPE, int WF = 1>
 struct MfmaShape {
     static constexpr int VPW = 32 / BITS;  // values per word
     static constexpr int VPC = 4 * VPW;    // values per 16-byte weight chunk (per lane half)
@@ -500,26 +510,47 @@ struct MfmaShape {
     static constexpr int SS = 2 * VPC;     // k per super-step
     static constexpr int SPS = XK / SS;    // super-steps per x stage
     static constexpr int ROWS = 32 * C;    // token rows per stage
-    // Several weight tiles per wave (A > 1): their chunks, scales and biases
-    // are prefetched one stage ahead into registers instead of the ring, which
-    // keeps the ring small enough for two workgroups per CU.
-    static constexpr bool WREG = A > 1;
+    static constexpr int KG = WK / WF;     // K-groups at most
+    // Several weight tiles per wave (A > 1) with one wave per x stage: their
+    // chunks are prefetched one stage ahead into registers instead of the
+    // ring, which keeps the ring small enough for two workgroups per CU.
+    static constexpr bool WREG = A > 1 && WF == 1;
     static constexpr int XST = ROWS * 128;                           // x tile bytes per stage
-    static constexpr int WST = WREG ? 0 : A * SPS * 1024;            // weight chunks per stage
-    static constexpr int SBST = WREG ? 0 : 2 * A * SPS * 256;        // scale and bias dwords
-    static constexpr int STAGE = XST + WST + SBST;      // one ring slot
-    static constexpr int XBYTES = WK * PIPE * STAGE;                  // stage rings
-    static constexpr int RBYTES = (WK - 1) * A * C * 16 * 64 * 4;     // K-split reduction
+    static constexpr int WAVE = WREG ? 0 : A * SPS * 1024;           // a wave's weight chunks
+    static constexpr int STAGE = XST + WF * WAVE;                    // one ring slot
+    static constexpr int XBYTES = KG * PIPE * STAGE;                 // stage rings
+    static constexpr int RBYTES = (KG - 1) * WF * A * C * 16 * 64 * 4;  // K-split reduction
     static constexpr int LDS = XBYTES > RBYTES ? XBYTES : RBYTES;
-    // DMA instructions a lane issues per stage: x, weights, scales, biases
-    static constexpr int OPS = ROWS / 8 + (WREG ? 0 : 3 * A * SPS);
+    // DMA instructions a lane issues per stage: its share of x, and weights
+    static constexpr int XOPS = ROWS / 8 / WF;
+    static constexpr int OPS = XOPS + (WREG ? 0 : A * SPS);
     // vmcnt at the top of a stage: the loads of the PIPE - 2 stages issued
     // after it may still be in flight (vmcnt decrements in issue order)
     static constexpr int VMCNT = (PIPE - 2) * OPS;
-    static_assert(PIPE >= 2 && PIPE <= 4 && VMCNT < 64, "vmcnt is a 6-bit count");
+    static_assert(WK % WF == 0 && (ROWS / 8) % WF == 0, "x instructions split evenly");
+    static_assert(PIPE >= 2 && PIPE <= MAX_PIPE && VMCNT < 64, "vmcnt is a 6-bit count");
     static_assert(!WREG || PIPE == 2, "register-prefetched weights run one stage ahead");
     static_assert(LDS <= LDS_PER_CU, "stage rings exceed the LDS of a CU");
 };
+
+// Scale/bias table of one wave: for each of its A weight tiles, the scales
+// then the biases of its 32 rows, pitch groups (2-byte values) per row,
+// starting at the even group at or below the wave's first group. The pitch
+// covers the wave's K slice plus the alignment group and is 2 mod 4, so the
+// 32 rows' reads of one column hit 32 distinct banks. Each array is copied
+// with 4-byte DMAs (two groups per lane, which needs an even number of
+// groups per weight row), padded to whole 64-lane instructions.
+struct SbtLayout {
+    int pitch;        // groups per row
+    int ninst;        // DMA instructions per array
+    int array_bytes;  // ninst * 256
+};
+__host__ __device__ inline SbtLayout sbt_layout(int64_t kslice, int gs) {
+    int need = (int)(kslice / gs) + 2;
+    need += ((2 - need) % 4 + 4) % 4;
+    const int ninst = (32 * need / 2 + 63) / 64;
+    return {need, ninst, ninst * 256};
+}
 
 // A raw buffer resource over [base, base + bytes): 32-bit offsets, and reads
 // past the end return zero instead of touching memory.
@@ -538,7 +569,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, 
 #define MI_QMM_MAX_PIPE 2
 #endif
 template <typename T, int BITS, int A, int C> constexpr int mfma_pipe() {
-    typedef MfmaShape<T, BITS, A, C, 4, 2> Sh2;
+    typedef MfmaShape<T, BITS, A, C, 4, 2, 1> Sh2;
     if constexpr (Sh2::WREG) return 2;
     constexpr int slot = Sh2::STAGE;
     constexpr int fit = 4 * 4 * slot <= LDS_PER_CU ? 4 : (4 * 3 * slot <= LDS_PER_CU ? 3 : 2);
@@ -552,12 +583,23 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-template <typename T, int BITS, int A, int C, int WK, int PIPE, int EPI>
+// Workgroup barrier with no memory fence: the waves have already waited for
+// their own DMAs into the stage (vmcnt), and LDS is one store per CU, so the
+// barrier alone makes the whole stage visible. (__syncthreads' fences would
+// also wait for the DMAs still filling the later slots.) The empty asm
+// statements keep the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void stage_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <typename T, int BITS, int A, int C, int WK, int PIPE, int EPI, int WF = 1>
 __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
     // The body uses gfx950 buffer resources, which the host target cannot
     // type; the host pass needs only the launch stub.
 #if defined(__HIP_DEVICE_COMPILE__)
-    typedef MfmaShape<T, BITS, A, C, WK, PIPE> Sh;
+    typedef MfmaShape<T, BITS, A, C, WK, PIPE, WF> Sh;
     constexpr int P = epi_parts(EPI);
     static_assert(P == 1 || A == P, "multi-part epilogues use one tile per part");
     constexpr int TN = (P == 1) ? A : 1;  // 32-wide output tiles per wave
@@ -566,12 +608,15 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
     __shared__ __attribute__((aligned(16))) char lds[Sh::LDS];
 
     const int lane = threadIdx.x & 63;
-    // the wave index is uniform per wave: in a scalar register, the x stage
-    // base addresses and the DMA's LDS destinations (M0) need no VALU work
-    const int kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // the wave indices are uniform per wave: in scalar registers, the x stage
+    // base addresses and the DMA's LDS destinations (M0) need no VALU work.
+    // Wave w owns feature tile fw = w % WF of the workgroup's WF tiles, in
+    // K-group kw = w / WF.
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int fw = wv % WF, kw = wv / WF;
     const int h = lane >> 5, r = lane & 31;
     const int64_t K = p.K, G = K / p.gs;
-    int64_t n_wave = (int64_t)blockIdx.x * (32 * TN);
+    int64_t n_wave = (int64_t)blockIdx.x * (32 * TN * WF) + fw * (32 * TN);
     const Bound bd = bind<EPI>(p, n_wave);
     const int64_t m_blk = (int64_t)blockIdx.y * (32 * C);
     const int wk = p.wk;
@@ -579,6 +624,7 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
     const int kbeg = kw * Kw;
     const int nst = Kw / XK;
     char *xbuf = lds + kw * PIPE * Sh::STAGE;
+    const int wslot = Sh::XST + fw * Sh::WAVE;  // this wave's weights within a slot
 
     // Rows past N (or tokens past M) read a clamped, valid row instead of
     // branching around the load: their accumulators only feed outputs the
@@ -586,7 +632,12 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
     // 2^32 (the host checks the sizes).
     const int gshift = p.gs_log2;
     __amdgpu_buffer_rsrc_t wr[A], sr[A], br[A];
-    uint32_t woff[A], sboff[A];
+    uint32_t woff[A];
+    auto tile_row = [&](int a, int rr) -> int64_t {  // weight-array row of tile row rr
+        const int part = (P == 1) ? 0 : a;
+        const int64_t nout = n_wave + ((P == 1) ? 32 * a : 0) + rr;
+        return bd.noff(part) + (nout < bd.Nout ? nout : bd.Nout - 1);
+    };
 #pragma unroll
     for (int a = 0; a < A; ++a) {
         const int part = (P == 1) ? 0 : a;
@@ -594,74 +645,83 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
         wr[a] = buffer_rsrc(bd.w(part), (uint32_t)(rows * K * BITS / 8));
         sr[a] = buffer_rsrc(bd.s(part), (uint32_t)(rows * G * 2));
         br[a] = buffer_rsrc(bd.b(part), (uint32_t)(rows * G * 2));
-        const int64_t nout = n_wave + ((P == 1) ? 32 * a : 0) + r;
-        const int64_t row = bd.noff(part) + (nout < bd.Nout ? nout : bd.Nout - 1);
-        woff[a] = (uint32_t)(row * (K * BITS / 8) + 16 * h);
-        // group of value k0 + h * VPC for a super-step start k0 (a multiple of
-        // 2 * VPC): k0 / gs, plus h when a group is no wider than a half-chunk
-        const int hg = (p.gs <= VPC) ? h * (VPC >> gshift) : 0;
-        sboff[a] = (uint32_t)((row * G + hg) * 2);
+        woff[a] = (uint32_t)(tile_row(a, r) * (K * BITS / 8) + 16 * h);
     }
+    // Scale/bias table (layout in sbt_layout): dword v of an array holds
+    // groups gbase + 2j, +1 of tile row v / (pitch / 2), j = v % (pitch / 2).
+    // Issued before the ring prologue, so the first stage's wait covers it.
+    const int pitch = p.sbp;
+    const SbtLayout tl = sbt_layout(Kw, p.gs);
+    extern __shared__ __attribute__((aligned(16))) char lds_dyn[];
+    const char *sbt = lds_dyn + wv * (A * 2 * tl.array_bytes);
+    const int gbase = (kbeg >> gshift) & ~1;
+    typedef __attribute__((address_space(3))) void *lds_ptr;
+    for (int i = 0; i < tl.ninst; ++i) {
+        int v = 64 * i + lane;
+        v = v < 16 * pitch ? v : 16 * pitch - 1;
+        const int rr = v / (pitch >> 1), j = v - rr * (pitch >> 1);
+#pragma unroll
+        for (int a = 0; a < A; ++a) {
+            const uint32_t off = (uint32_t)((tile_row(a, rr) * G + gbase + 2 * j) * 2);
+            char *dst = (char *)sbt + (2 * a) * tl.array_bytes + i * 256;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(sr[a], (lds_ptr)dst, 4, off, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(br[a], (lds_ptr)(dst + tl.array_bytes), 4, off,
+                                                     0, 0, 0);
+        }
+    }
+    // group of value k0 + h * VPC for a super-step start k0 (a multiple of
+    // 2 * VPC): k0 / gs, plus h when a group is no wider than a half-chunk;
+    // as a byte offset into the table, relative to gbase
+    const int hg = (p.gs <= VPC) ? h * (VPC >> gshift) : 0;
+    const int sbrow = (r * pitch + hg - gbase) * 2;
     // x DMA: instruction i writes stage rows 8i..8i+7; lane l fills row
     // 8i + l/8 at swizzled position l%8, i.e. it loads chunk (l%8) ^ swz(row).
+    // Wave fw issues instructions i = WF * j + fw.
     const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(p.x, (uint32_t)(p.M * K * (int64_t)sizeof(T)));
-    uint32_t xoff[C * 4];
+    uint32_t xoff[Sh::XOPS];
 #pragma unroll
-    for (int i = 0; i < C * 4; ++i) {
-        const int row = 8 * i + (lane >> 3);
+    for (int j = 0; j < Sh::XOPS; ++j) {
+        const int row = 8 * (WF * j + fw) + (lane >> 3);
         const int64_t m = m_blk + row < p.M ? m_blk + row : p.M - 1;
         const int chunk = (lane & 7) ^ ((row >> 1) & 7);
-        xoff[i] = (uint32_t)((m * K + 8 * chunk) * (int64_t)sizeof(T));
+        xoff[j] = (uint32_t)((m * K + 8 * chunk) * (int64_t)sizeof(T));
     }
-    typedef __attribute__((address_space(3))) void *lds_ptr;
     auto issue = [&](int st, char *slot) {
         const int k0 = kbeg + st * XK;
         const uint32_t xs = (uint32_t)k0 * sizeof(T);
 #pragma unroll
-        for (int i = 0; i < C * 4; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(slot + i * 1024), 16, xoff[i],
+        for (int j = 0; j < Sh::XOPS; ++j)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(slot + (WF * j + fw) * 1024), 16,
+                                                     xoff[j],
                                                      xs, 0, 0);
         if constexpr (Sh::WREG) return;
 #pragma unroll
         for (int u = 0; u < SPS; ++u) {
             const int ku = k0 + u * SS;
             const uint32_t ws = (uint32_t)(ku / VPW) * 4;
-            const uint32_t gsoff = (uint32_t)(ku >> gshift) * 2;
 #pragma unroll
             for (int a = 0; a < A; ++a) {
-                char *wdst = slot + Sh::XST + (a * SPS + u) * 1024;
-                char *sdst = slot + Sh::XST + Sh::WST + (a * SPS + u) * 512;
+                char *wdst = slot + wslot + (a * SPS + u) * 1024;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(wr[a], (lds_ptr)wdst, 16, woff[a], ws, 0, 0);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(sr[a], (lds_ptr)sdst, 2, sboff[a], gsoff,
-                                                         0, 0);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(br[a], (lds_ptr)(sdst + 256), 2, sboff[a],
-                                                         gsoff, 0, 0);
             }
         }
     };
-    // WREG: the weight chunks, scales and biases of a stage into registers
+    // WREG: the weight chunks of a stage into registers
     uint4 wreg[2][A][SPS];
-    uint16_t sreg[2][A][SPS], breg[2][A][SPS];
-    const char *wlane[A], *slane[A], *blane[A];
+    const char *wlane[A];
 #pragma unroll
     for (int a = 0; a < A; ++a) {
         const int part = (P == 1) ? 0 : a;
         wlane[a] = (const char *)bd.w(part) + woff[a];
-        slane[a] = (const char *)bd.s(part) + sboff[a];
-        blane[a] = (const char *)bd.b(part) + sboff[a];
     }
-    auto load_w = [&](int st, uint4 (&wd)[A][SPS], uint16_t (&sd)[A][SPS],
-                      uint16_t (&bd_)[A][SPS]) {
+    auto load_w = [&](int st, uint4 (&wd)[A][SPS]) {
 #pragma unroll
         for (int u = 0; u < SPS; ++u) {
             const int ku = kbeg + st * XK + u * SS;
             const uint32_t ws = (uint32_t)(ku / VPW) * 4;
-            const uint32_t gsoff = (uint32_t)(ku >> gshift) * 2;
 #pragma unroll
             for (int a = 0; a < A; ++a) {
                 wd[a][u] = ld16(wlane[a] + ws);
-                sd[a][u] = *(const uint16_t *)(slane[a] + gsoff);
-                bd_[a][u] = *(const uint16_t *)(blane[a] + gsoff);
             }
         }
     };
@@ -676,31 +736,41 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
 
     // Pipeline, PIPE stages deep: while stage st computes, the DMAs of stage
     // st + PIPE - 1 fill ring slot (st + PIPE - 1) % PIPE, which was last read
-    // by stage st - 1 (its ds_reads completed before its MFMAs). Every stage
-    // issues exactly OPS DMAs -- past the last stage they re-read stage
-    // nst - 1, in bounds, into slots no later stage reads -- so at the top of
-    // stage st at most the loads of the PIPE - 2 stages after it are in
-    // flight: vmcnt(VMCNT). The stage loop is unrolled PIPE times so each
-    // slot is named statically.
+    // by stage st - 1 (its ds_reads completed before its MFMAs; with WF > 1
+    // the barrier at the top of stage st also waits for the other waves to
+    // finish stage st - 1). Every stage issues exactly OPS DMAs -- past the
+    // last stage they re-read stage nst - 1, in bounds, into slots no later
+    // stage reads -- so at the top of stage st at most the loads of the
+    // PIPE - 2 stages after it are in flight: vmcnt(VMCNT). The stage loop is
+    // unrolled PIPE times so each slot is named statically.
     //
-    // The slots are passed as separate __restrict__ arguments of the inlined
-    // main loop: the resulting alias scopes let the compiler's wait-count
-    // pass see that a stage's ds_reads cannot touch the slots the DMAs in
-    // flight are filling, so it adds no vmcnt(0) of its own before them.
+    // The slots (and the scale/bias table) are passed as separate __restrict__
+    // arguments of the inlined main loop: the resulting alias scopes let the
+    // compiler's wait-count pass see that a stage's ds_reads cannot touch the
+    // slots the DMAs in flight are filling, so it adds no vmcnt(0) of its own
+    // before them. The table's DMAs precede the ring prologue's, so the wait
+    // at the top of stage 0 retires them.
     const int swz = (r >> 1) & 7;
+    const int tab = tl.array_bytes;
     auto mainloop = [&](char *__restrict__ b0, char *__restrict__ b1, char *__restrict__ b2,
-                        char *__restrict__ b3) __attribute__((always_inline)) {
-    auto ring = [&](int j) -> char * { return j == 0 ? b0 : (j == 1 ? b1 : (j == 2 ? b2 : b3)); };
+                        char *__restrict__ b3, char *__restrict__ b4, char *__restrict__ b5,
+                        char *__restrict__ b6, char *__restrict__ b7,
+                        const char *__restrict__ tb) __attribute__((always_inline)) {
+    auto ring = [&](int j) -> char * {
+        return j == 0 ? b0 : j == 1 ? b1 : j == 2 ? b2 : j == 3 ? b3 : j == 4 ? b4 : j == 5 ? b5
+               : j == 6 ? b6 : b7;
+    };
     const int last = nst > 0 ? nst - 1 : 0;
 #pragma unroll
     for (int j = 0; j < PIPE - 1; ++j) issue(j < last ? j : last, ring(j));
-    if constexpr (Sh::WREG) load_w(0, wreg[0], sreg[0], breg[0]);
+    if constexpr (Sh::WREG) load_w(0, wreg[0]);
     for (int st0 = 0; st0 < nst; st0 += PIPE) {
 #pragma unroll
         for (int j = 0; j < PIPE; ++j) {
             const int st = st0 + j;
-            if (st >= nst) break;  // wave-uniform
+            if (st >= nst) break;  // workgroup-uniform
             wait_vmcnt<Sh::VMCNT>();
+            if constexpr (WF > 1) stage_barrier();
             const char *cur = ring(j);
             uint4 xf[C][SPS][S];
 #pragma unroll
@@ -719,21 +789,19 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
             for (int a = 0; a < A; ++a)
 #pragma unroll
                 for (int u = 0; u < SPS; ++u) {
-                    if constexpr (Sh::WREG) {
+                    if constexpr (Sh::WREG)
                         wq[a][u] = wreg[j][a][u];
-                        sq[a][u] = sreg[j][a][u];
-                        bq[a][u] = breg[j][a][u];
-                    } else {
-                        wq[a][u] = *(const uint4 *)(cur + Sh::XST + (a * SPS + u) * 1024 + lane * 16);
-                        const char *sb = cur + Sh::XST + Sh::WST + (a * SPS + u) * 512;
-                        sq[a][u] = *(const uint32_t *)(sb + lane * 4);
-                        bq[a][u] = *(const uint32_t *)(sb + 256 + lane * 4);
-                    }
+                    else
+                        wq[a][u] = *(const uint4 *)(cur + wslot + (a * SPS + u) * 1024 + lane * 16);
+                    const char *sb = tb + 2 * a * tab + sbrow +
+                                     ((kbeg + st * XK + u * SS) >> gshift) * 2;
+                    sq[a][u] = *(const uint16_t *)sb;
+                    bq[a][u] = *(const uint16_t *)(sb + tab);
                 }
             const int nx = st + PIPE - 1 < last ? st + PIPE - 1 : last;
             issue(nx, ring((j + PIPE - 1) % PIPE));
             if constexpr (Sh::WREG) {  // PIPE == 2: the next stage, into the other set
-                load_w(nx, wreg[(j + 1) % 2], sreg[(j + 1) % 2], breg[(j + 1) % 2]);
+                load_w(nx, wreg[(j + 1) % 2]);
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -757,13 +825,16 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
         }
     }
     };
+    // (slots past PIPE are never named; they alias slot 0)
     mainloop(xbuf, xbuf + (PIPE > 1 ? 1 : 0) * Sh::STAGE, xbuf + (PIPE > 2 ? 2 : 0) * Sh::STAGE,
-             xbuf + (PIPE > 3 ? 3 : 0) * Sh::STAGE);
+             xbuf + (PIPE > 3 ? 3 : 0) * Sh::STAGE, xbuf + (PIPE > 4 ? 4 : 0) * Sh::STAGE,
+             xbuf + (PIPE > 5 ? 5 : 0) * Sh::STAGE, xbuf + (PIPE > 6 ? 6 : 0) * Sh::STAGE,
+             xbuf + (PIPE > 7 ? 7 : 0) * Sh::STAGE, sbt);
     // the loads issued past the last stage land before the LDS is reused for
     // the reduction or released with the workgroup
     wait_vmcnt<0>();
 
-    if constexpr (WK > 1) {
+    if constexpr (Sh::KG > 1) {
         // fixed-order reduction of the K-split partial tiles; the LDS staging
         // is reused, so every wave must be done with its x stages first
         constexpr int REGS = A * C * 16;
@@ -771,7 +842,7 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
         __syncthreads();
         if (wk > 1) {
             if (kw > 0) {
-                float *dst = red + (size_t)(kw - 1) * REGS * 64 + lane;
+                float *dst = red + (size_t)((kw - 1) * WF + fw) * REGS * 64 + lane;
 #pragma unroll
                 for (int a = 0; a < A; ++a)
 #pragma unroll
@@ -782,7 +853,7 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
             __syncthreads();
             if (kw > 0) return;
             for (int src = 1; src < wk; ++src) {
-                const float *sp = red + (size_t)(src - 1) * REGS * 64 + lane;
+                const float *sp = red + (size_t)((src - 1) * WF + fw) * REGS * 64 + lane;
 #pragma unroll
                 for (int a = 0; a < A; ++a)
 #pragma unroll
@@ -840,14 +911,29 @@ int launch_qmv(const QParams &p, hipStream_t st) {
     return launch_status("quantized matmul (qmv)");
 }
 
+// LDS of one workgroup: the static stage rings plus the waves' scale/bias
+// tables (dynamic).
+template <typename T, int BITS, int A, int C>
+int64_t mfma_lds_bytes(const QParams &p, int wk) {
+    constexpr int PIPE = mfma_pipe<T, BITS, A, C>();
+    const SbtLayout tl = sbt_layout(p.K / wk, p.gs);
+    return MfmaShape<T, BITS, A, C, 4, PIPE>::LDS + (int64_t)wk * A * 2 * tl.array_bytes;
+}
+
 template <typename T, int BITS, int A, int C, int EPI>
 int launch_mfma_cfg(QParams p, int wk, hipStream_t st) {
     constexpr int P = epi_parts(EPI);
     constexpr int TN = (P == 1) ? A : 1;
     constexpr int PIPE = mfma_pipe<T, BITS, A, C>();
     p.wk = wk;
+    const SbtLayout tl = sbt_layout(p.K / wk, p.gs);
+    p.sbp = tl.pitch;
+    const size_t dyn = (size_t)wk * A * 2 * tl.array_bytes;
+    if (mfma_lds_bytes<T, BITS, A, C>(p, wk) > LDS_PER_CU)
+        return fail(MI_ERR_UNSUPPORTED, "quantized matmul tile exceeds the LDS (K = %lld)",
+                    (long long)p.K);
     const dim3 grid((unsigned)ceil_div(p.Nout, 32 * TN), (unsigned)ceil_div(p.M, 32 * C));
-    qmm_mfma_kernel<T, BITS, A, C, 4, PIPE, EPI><<<grid, 64 * wk, 0, st>>>(p);
+    qmm_mfma_kernel<T, BITS, A, C, 4, PIPE, EPI><<<grid, 64 * wk, dyn, st>>>(p);
     return launch_status("quantized matmul (mfma)");
 }
 
@@ -858,7 +944,9 @@ int launch_mfma_cfg(QParams p, int wk, hipStream_t st) {
 // would leave fewer than 128 workgroups (half the CUs), and 64x128 tiles once
 // the grid exceeds 2048 workgroups (large M), where re-reading x per narrow
 // tile costs more than the lost parallelism.
-// K must split into wk slices of whole 64-value x stages.
+// K must split into wk slices of whole 64-value x stages. A tile whose rings
+// and scale/bias tables (which grow with K) exceed the LDS steps down to the
+// next smaller one, and past the smallest the GEMV kernel runs instead.
 template <typename T, int BITS, int EPI>
 int launch_mfma(const QParams &p, hipStream_t st) {
     constexpr int P = epi_parts(EPI);
@@ -866,13 +954,18 @@ int launch_mfma(const QParams &p, hipStream_t st) {
     const int wk = (stages % 4 == 0) ? 4 : (stages % 2 == 0 ? 2 : 1);
     const int64_t nt = ceil_div(p.Nout, 32);
     if constexpr (P == 1) {
-        if (nt * ceil_div(p.M, 64) > 2048 && EPI != EPI_GROUP3)
-            // (8-bit: 32x128, whose stage slots still fit the LDS twice)
-            return launch_mfma_cfg<T, BITS, BITS == 4 ? 2 : 1, 4, EPI>(p, wk, st);
+        // (8-bit: 32x128, whose stage slots still fit the LDS twice)
+        constexpr int AL = BITS == 4 ? 2 : 1;
+        if (nt * ceil_div(p.M, 64) > 2048 && EPI != EPI_GROUP3 &&
+            mfma_lds_bytes<T, BITS, AL, 4>(p, wk) <= LDS_PER_CU)
+            return launch_mfma_cfg<T, BITS, AL, 4, EPI>(p, wk, st);
     }
-    if (p.M > 32 && nt * ceil_div(p.M, 64) >= 128)
+    if (p.M > 32 && nt * ceil_div(p.M, 64) >= 128 &&
+        mfma_lds_bytes<T, BITS, P, 2>(p, wk) <= LDS_PER_CU)
         return launch_mfma_cfg<T, BITS, P, 2, EPI>(p, wk, st);
-    return launch_mfma_cfg<T, BITS, P, 1, EPI>(p, wk, st);
+    if (mfma_lds_bytes<T, BITS, P, 1>(p, wk) <= LDS_PER_CU)
+        return launch_mfma_cfg<T, BITS, P, 1, EPI>(p, wk, st);
+    return launch_qmv<T, BITS, EPI>(p, st);
 }
 
 template <typename T, int EPI>
@@ -892,8 +985,9 @@ template <typename T, int EPI>
 int launch_typed(const QParams &p, int bits, hipStream_t st) {
     // the MFMA kernel addresses x and each weight array with 32-bit offsets
     const int64_t wrows = p.noff[2] + p.Nout;  // rows of the largest part's arrays
+    // and copies scale/bias pairs with 4-byte loads (an even group count)
     const bool mfma = (sizeof(T) == 2) && p.M > QMV_MR && (p.K % XK == 0) &&
-                      p.M * p.K < ((int64_t)1 << 31) &&
+                      (p.K / p.gs) % 2 == 0 && p.M * p.K < ((int64_t)1 << 31) &&
                       wrows * p.K * bits / 8 < ((int64_t)1 << 32);
     if constexpr (sizeof(T) == 2) {
         const int mr = p.M == 1 ? 1 : (p.M == 2 ? 2 : 4);
