@@ -17,6 +17,9 @@ Also measured live, with HIP events on the stream the kernels run on:
   - qmm: the benchmark's config 2 (x[M, 2560] @ W[9728, 2560]^T, 4-bit g64) at M=1
     (HBM GB/s vs 8 TB/s) and M=128 (TFLOP/s vs the MFMA peak), rotating more
     weight copies than the 256 MB Infinity Cache holds;
+  - lfm2_config5: the benchmark's config 5 beside the headline, the
+    LFM2-1.2B-shaped hybrid prefilling 2048 tokens, 4- and 8-bit (ms per
+    prefill and tok/s, one HIP-graph replay each);
   - cpu_baseline: the CPU oracle (the port; MLX is not installed) on a bounded
     sample -- one decoder layer at L=128 plus the lm_head for one token --
     scaled to the 36-layer model.
@@ -196,6 +199,41 @@ def cpu_baseline(model, ids, torch):
                       "unavailable (mlx not installed, no network)"}
 
 
+def lfm2_config5(torch, ops, reps: int = 10) -> dict:
+    """Config 5 beside the headline: the LFM2-1.2B-shaped hybrid (16 layers:
+    10 gated short-conv, 6 attention; hidden 2048, SwiGLU 8192, tied
+    V = 65536) prefilling 2048 seeded token ids, 4- and 8-bit, region cuts
+    installed; one HIP-graph replay per prefill, timed with HIP events."""
+    from workloads import lfm2, qwen3
+
+    out = {"workload": "config 5: LFM2-1.2B-shaped hybrid, 16 layers, g64, tied V=65536, "
+                       "prefill of 2048 seeded token ids (lm_head on the last position)"}
+    for bits in (4, 8):
+        cfg = lfm2.Lfm2Config(bits=bits)
+        model = lfm2.build(cfg, seed=0)
+        lfm2.install_regions(model)
+        ids = qwen3.tokens(2, 2048, cfg.vocab_size)
+        caches = model.make_cache(2048)
+
+        def step():
+            for c in caches:
+                c.offset = 0
+                if isinstance(c, lfm2.ConvCache):
+                    c.state = None
+            return ops.argmax(model(ids, caches).reshape(1, -1))
+
+        g, tok = graph_of(step, torch)
+        g.replay()
+        torch.cuda.synchronize()
+        ms = time_graph(g, reps, torch)
+        out[f"{bits}bit"] = {"ms_per_prefill": round(ms, 3),
+                             "tok_s": round(2048 / (ms / 1000.0), 1),
+                             "greedy_token": int(tok.item())}
+        del g, model, caches
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -239,6 +277,9 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(model, ids, torch)
+    del g, model, caches
+    torch.cuda.empty_cache()
+    hybrid = lfm2_config5(torch, ops)
     line = {
         "metric": "prefill tok/s Qwen3-4B-shape 4-bit @128 tok; qmm HBM GB/s and MFMA % of peak",
         "value": round(PROMPT / (ms / 1000.0), 1),
@@ -259,6 +300,7 @@ def main():
                    "greedy_token": token},
         "roofline": roof,
         "qmm": qmm,
+        "lfm2_config5": hybrid,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -50,6 +50,14 @@ Pins (all in tests/test_oracle.py):
                       (its fused-kernel rounding) is parity unpinned.
   qwen3_forward       no-layer case: tied head over the dequantized table
                       row of the last id.
+  lfm2_conv_layer,    op streams of the reference's LFM2 wrappers (cited per
+  lfm2_attn_layer     function), composed of the pinned primitives above;
+                      pinned by structure checks: zero out_proj and w2 ->
+                      identity exactly; a conv layer run in two chunks with
+                      the state carried == one run over the whole sequence;
+                      an attention decode at offset L == the last row of an
+                      (L+1)-token prefill. Bitwise agreement with MLX's own
+                      LFM2 layers is parity unpinned.
 """
 
 from __future__ import annotations
@@ -457,3 +465,57 @@ def qwen3_forward(ids, layers: list, embed, final_norm, cfg, offset: int, kcache
         h = qwen3_layer(h, W, cfg, offset, kcaches[i], vcaches[i], dtype)
     hn = rms_norm(h[:, -1:], final_norm, cfg.rms_norm_eps, dtype)
     return qmm_factored(hn, wq, s, b, cfg.group_size, cfg.bits, dtype)
+
+
+# ----------------------------------------------------------------------------
+# LFM2 hybrid (config 5): the op streams of the reference's generated
+# wrappers, examples/lfm2_5_1_2b_prefill/lfm2_5_1_2b_prefill_artifact/
+# patch/wrappers.py (conv layers :38-106, attention layers :145-220)
+
+
+def lfm2_mlp(hn, h, W: dict, cfg, dtype: str = "bfloat16"):
+    """[qmm(w1), qmm(w3)] -> swiglu -> [qmm(w2), add] (wrappers.py:81-106)."""
+    gs, bits = cfg.group_size, cfg.bits
+    g = _qmm_auto(hn, W["w1"], gs, bits, dtype)
+    u = _qmm_auto(hn, W["w3"], gs, bits, dtype)
+    d = _qmm_auto(swiglu(g, u, dtype), W["w2"], gs, bits, dtype)
+    return round_to(np.asarray(h, np.float64) + d, dtype)
+
+
+def lfm2_conv_layer(x, W: dict, cfg, state, dtype: str = "bfloat16"):
+    """Gated short-conv layer (wrappers.py:38-106): rms_norm(operator_norm) ->
+    qmm(in_proj) -> split(3) = (B, C, x) -> B*x -> conv over
+    concat(state or zeros, B*x) -> C*conv -> qmm(out_proj) + residual ->
+    rms_norm(ffn_norm) -> MLP + residual. W["conv"] is the [D, 3] depthwise
+    weight. Returns (layer output, new conv state)."""
+    gs, bits, eps = cfg.group_size, cfg.bits, cfg.norm_eps
+    xn = rms_norm(x, W["operator_norm"], eps, dtype)
+    c, bx = split_gate(_qmm_auto(xn, W["in_proj"], gs, bits, dtype), dtype)
+    y, new_state = shortconv(bx, c, W["conv"], state, dtype)
+    h = round_to(np.asarray(x, np.float64) + _qmm_auto(y, W["out_proj"], gs, bits, dtype), dtype)
+    hn = rms_norm(h, W["ffn_norm"], eps, dtype)
+    return lfm2_mlp(hn, h, W, cfg, dtype), new_state
+
+
+def lfm2_attn_layer(x, W: dict, cfg, offset: int, kcache, vcache, dtype: str = "bfloat16"):
+    """Attention layer (wrappers.py:145-220): rms_norm(operator_norm) ->
+    q/k/v qmm -> per-head rms_norm(q_layernorm / k_layernorm) -> rope (head
+    dim, base rope_theta, offset) -> cache update -> causal sdpa (scale
+    head_dim^-0.5) -> qmm(out_proj) + residual -> rms_norm(ffn_norm) -> MLP +
+    residual. kcache/vcache [1, HK, cap, D] are written at [offset, offset+L)."""
+    gs, bits, eps = cfg.group_size, cfg.bits, cfg.norm_eps
+    H, HK, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    L = x.shape[1]
+    xn = rms_norm(x, W["operator_norm"], eps, dtype)
+    q = _qmm_auto(xn, W["q_proj"], gs, bits, dtype)
+    k = _qmm_auto(xn, W["k_proj"], gs, bits, dtype)
+    v = _qmm_auto(xn, W["v_proj"], gs, bits, dtype)
+    qr = norm_rope(q, W["q_layernorm"], eps, H, D, cfg.rope_theta, offset, dtype)
+    kcache[:, :, offset:offset + L] = norm_rope(k, W["k_layernorm"], eps, HK, D, cfg.rope_theta,
+                                                offset, dtype)
+    vcache[:, :, offset:offset + L] = norm_rope(v, None, 0.0, HK, 0, 1.0, 0, dtype)
+    o = sdpa(qr, kcache[:, :, :offset + L], vcache[:, :, :offset + L], D ** -0.5, L > 1, dtype)
+    o = np.ascontiguousarray(np.transpose(o, (0, 2, 1, 3))).reshape(1, L, H * D)
+    h = round_to(np.asarray(x, np.float64) + _qmm_auto(o, W["out_proj"], gs, bits, dtype), dtype)
+    hn = rms_norm(h, W["ffn_norm"], eps, dtype)
+    return lfm2_mlp(hn, h, W, cfg, dtype)

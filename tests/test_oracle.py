@@ -404,3 +404,77 @@ def test_forward_embedding_gather_and_tied_head():
     assert logits.shape == (1, 1, V)
     err = np.abs(logits - want).max() / np.abs(want).max()
     assert err < 1e-2
+
+
+# ---------------------------------------------------------------------- LFM2
+
+
+def _tiny_lfm2(seed, hidden=128, inter=256, zero=()):
+    from types import SimpleNamespace
+
+    cfg = SimpleNamespace(group_size=64, bits=4, norm_eps=1e-5, num_attention_heads=4,
+                          num_key_value_heads=2, head_dim=32, rope_theta=1e6)
+    r = rng(seed)
+    H, HK, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    shapes = {"in_proj": (3 * hidden, hidden), "out_proj": (hidden, H * D),
+              "q_proj": (H * D, hidden), "k_proj": (HK * D, hidden), "v_proj": (HK * D, hidden),
+              "w1": (inter, hidden), "w3": (inter, hidden), "w2": (hidden, inter)}
+    W = {}
+    for name, (n, k) in shapes.items():
+        wq, s, b = oracle.quantize_affine(r.normal(0, 0.05, (n, k)).astype(np.float32), 64, 4,
+                                          "bfloat16")
+        if name in zero:
+            s, b = np.zeros_like(s), np.zeros_like(b)
+        W[name] = (wq, s, b)
+    for name, d in (("q_layernorm", D), ("k_layernorm", D), ("operator_norm", hidden),
+                    ("ffn_norm", hidden)):
+        W[name] = oracle.round_to(1 + 0.1 * r.normal(0, 1, d), "bfloat16")
+    W["conv"] = oracle.round_to(0.3 * r.normal(0, 1, (hidden, 3)), "bfloat16")
+    return cfg, W
+
+
+def test_lfm2_layers_residual_structure():
+    """out_proj and w2 dequantizing to zero: both LFM2 layer kinds are the
+    identity, exactly, and the conv layer still hands on its last two B*x
+    rows as the state."""
+    cfg, W = _tiny_lfm2(50, zero=("out_proj", "w2"))
+    x = oracle.round_to(rng(51).normal(0, 1, (1, 5, 128)), "bfloat16")
+    y, st = oracle.lfm2_conv_layer(x, W, cfg, None)
+    assert np.array_equal(y, x)
+    xn = oracle.rms_norm(x, W["operator_norm"], cfg.norm_eps, "bfloat16")
+    _, bx = oracle.split_gate(oracle._qmm_auto(xn, W["in_proj"], 64, 4, "bfloat16"), "bfloat16")
+    assert np.array_equal(st, bx[:, -2:])
+    kc, vc = _caches(cfg)
+    assert np.array_equal(oracle.lfm2_attn_layer(x, W, cfg, 0, kc, vc), x)
+
+
+@pytest.mark.parametrize("split", [1, 2, 4])
+def test_lfm2_conv_layer_chunks_equal_whole(split):
+    """A 7-row sequence through the conv layer in two chunks, the state
+    carried, is bit-identical to one pass (a state taken from B*x alone, or
+    the wrong rows of it, fails when the first chunk is shorter than 2)."""
+    cfg, W = _tiny_lfm2(52)
+    x = oracle.round_to(rng(53).normal(0, 1, (1, 7, 128)), "bfloat16")
+    whole, st_whole = oracle.lfm2_conv_layer(x, W, cfg, None)
+    a, st = oracle.lfm2_conv_layer(x[:, :split], W, cfg, None)
+    b, st2 = oracle.lfm2_conv_layer(x[:, split:], W, cfg, st)
+    assert np.array_equal(np.concatenate([a, b], axis=1), whole)
+    assert np.array_equal(st2, st_whole)
+
+
+def test_lfm2_attn_decode_equals_prefill_last_row():
+    """The LFM2 attention layer: a 5-token prefix fills the cache, the 6th
+    token decoded at offset 5 matches the last row of a 6-token prefill; a
+    wrong rope offset is far outside that bar."""
+    cfg, W = _tiny_lfm2(54)
+    seq = oracle.round_to(rng(55).normal(0, 1, (1, 6, 128)), "bfloat16")
+    kc, vc = _caches(cfg)
+    full = oracle.lfm2_attn_layer(seq, W, cfg, 0, kc, vc)
+    kc2, vc2 = _caches(cfg)
+    oracle.lfm2_attn_layer(seq[:, :5], W, cfg, 0, kc2, vc2)
+    last = oracle.lfm2_attn_layer(seq[:, 5:], W, cfg, 5, kc2, vc2)
+    assert np.abs(last - full[:, 5:]).max() / np.abs(full[:, 5:]).max() < 1e-2
+    kc3, vc3 = _caches(cfg)
+    oracle.lfm2_attn_layer(seq[:, :5], W, cfg, 0, kc3, vc3)
+    wrong = oracle.lfm2_attn_layer(seq[:, 5:], W, cfg, 0, kc3, vc3)
+    assert np.abs(wrong - full[:, 5:]).max() / np.abs(full[:, 5:]).max() > 1e-2
