@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-lfm2", action="store_true",
+                    help="skip the config 5 measurement (keeps a kernel trace to the headline model)")
     return ap.parse_args()
 
 
@@ -279,7 +281,7 @@ def main():
         cpu = cpu_baseline(model, ids, torch)
     del g, model, caches
     torch.cuda.empty_cache()
-    hybrid = lfm2_config5(torch, ops)
+    hybrid = None if args.no_lfm2 else lfm2_config5(torch, ops)
     line = {
         "metric": "prefill tok/s Qwen3-4B-shape 4-bit @128 tok; qmm HBM GB/s and MFMA % of peak",
         "value": round(PROMPT / (ms / 1000.0), 1),
