@@ -136,32 +136,45 @@ __global__ __launch_bounds__(256) void attn_kernel(const T *__restrict__ q,
             const V8 a = __builtin_bit_cast(V8, *(const uint4 *)(ks + r * KP + 16 * st + 8 * h2));
             s = AMfma<T>::mma(a, __builtin_bit_cast(V8, qf[st]), s);
         }
-        // s[i]: key kt*32 + 8*(i/4) + 4*h2 + i%4 of query row qrow
+        // s[i]: key kt*32 + 8*(i/4) + 4*h2 + i%4 of query row qrow. A tile
+        // whose every key every row of the block sees needs no mask.
         float p[16];
         float mt = -INFINITY;
+        const bool full = (int64_t)kt * KT + KT <= Lk &&
+                          (!causal || (int64_t)kt * KT + KT - 1 <= q0 + off);
+        const int vis_end = (int)((causal && qrow + off + 1 < Lk ? qrow + off + 1 : Lk) -
+                                  (int64_t)kt * KT);  // keys [0, vis_end) of the tile
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const int64_t kg = (int64_t)kt * KT + 8 * (i / 4) + 4 * h2 + (i % 4);
-            const bool vis = kg < Lk && (!causal || kg <= qrow + off);
-            p[i] = vis ? s[i] * scale_log2 : -INFINITY;
+            const int kl = 8 * (i / 4) + 4 * h2 + (i % 4);
+            p[i] = (full || kl < vis_end) ? s[i] * scale_log2 : -INFINITY;
             mt = fmaxf(mt, p[i]);
         }
         mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-        const float m_new = fmaxf(m_run, mt);
-        const bool none = m_new == -INFINITY;
-        const float corr = none ? 1.0f : exp2f(m_run - m_new);
+        // Lazy rescale: the exponents are taken against a running reference
+        // m_run that moves only when a row's maximum passes it by more than
+        // 8 (log2 units). p then stays below 2^8, where fp32 sums and the
+        // bf16/fp16 P operand keep their relative precision, and the 64
+        // accumulator rescales run only on those (wave-uniform) steps.
+        const bool grow = mt > m_run + 8.0f;
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+            const float m_new = grow ? mt : m_run;
+            const float corr = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= corr;
+#pragma unroll
+            for (int t = 0; t < DT; ++t)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[t][i] *= corr;
+            m_run = m_new;
+        }
+        const bool none = m_run == -INFINITY;
         float psum = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            p[i] = none ? 0.0f : exp2f(p[i] - m_new);
+            p[i] = none ? 0.0f : __builtin_amdgcn_exp2f(p[i] - m_run);
             psum += p[i];
         }
-        l_run = l_run * corr + psum;
-        m_run = m_new;
-#pragma unroll
-        for (int t = 0; t < DT; ++t)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) o[t][i] *= corr;
+        l_run += psum;
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
             V8 pb;

@@ -321,7 +321,13 @@ constexpr int QV_BATCH = 8;  // 16-byte weight chunks in flight per lane
 
 inline int64_t qmv_dot2_lds_bytes(int mr, int64_t K) { return mr * K * 2 + mr * (K / 32) * 4; }
 
-template <typename T, int MR, int EPI>
+// PF: the x loads, then the first weight batch, are issued before x is
+// staged, so the weight stream runs under the staging and its two barriers
+// (x first: vmcnt retires in issue order, so waiting for x then leaves the
+// weights in flight). Each thread holds at most two x chunks (MR * K / 8 <=
+// 512). It costs the batch registers through the staging, which pays when
+// the grid fits the chip in one round and not at N = 151936.
+template <typename T, int MR, int EPI, bool PF = false>
 __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
     constexpr int P = epi_parts(EPI);
     typedef Magic<T> Mg;
@@ -347,9 +353,6 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
         br[q] = (const T *)bd.b(q) + row * G;
     }
 
-    // (Requesting the first weight batch before x is staged was measured: it
-    // holds the batch registers through the staging, and the lost occupancy
-    // cost more at N = 151936 than the overlap gained at N = 9728.)
     uint4 wv[P][QV_BATCH];
     T sv[P][QV_BATCH], bv[P][QV_BATCH];
     auto load_batch = [&](int64_t base) {
@@ -369,13 +372,37 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
 
     // stage x rows as pairs (e[i], e[i+4]) of each 8-value block
     const T *x = (const T *)p.x + m0 * K;
-    for (int64_t idx = threadIdx.x; idx < MR * words; idx += 256) {
-        const int64_t m = idx / words, w = idx - m * words;
-        const uint4 d = ld16(x + (m < mr ? m : mr - 1) * K + 8 * w);
-        xs_pairs[idx] = make_uint4(__builtin_amdgcn_perm(d.z, d.x, 0x05040100u),
-                                   __builtin_amdgcn_perm(d.z, d.x, 0x07060302u),
-                                   __builtin_amdgcn_perm(d.w, d.y, 0x05040100u),
-                                   __builtin_amdgcn_perm(d.w, d.y, 0x07060302u));
+    auto pairs = [](const uint4 d) {
+        return make_uint4(__builtin_amdgcn_perm(d.z, d.x, 0x05040100u),
+                          __builtin_amdgcn_perm(d.z, d.x, 0x07060302u),
+                          __builtin_amdgcn_perm(d.w, d.y, 0x05040100u),
+                          __builtin_amdgcn_perm(d.w, d.y, 0x07060302u));
+    };
+    if constexpr (PF) {
+        // every thread issues both loads (a clamped, valid chunk when past the
+        // end) so the issue order, and with it the waits, is the same in all
+        // waves: x, then the weights
+        uint4 d[2];
+        const int nw = (int)words;  // <= 512 here: 32-bit index math
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            int idx = (int)threadIdx.x + 256 * t;
+            idx = idx < MR * nw ? idx : MR * nw - 1;
+            const int m = MR == 1 ? 0 : idx / nw, w = idx - m * nw;
+            d[t] = ld16(x + (int64_t)(m < mr ? m : mr - 1) * K + 8 * w);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep the x loads ahead of the weights'
+        load_batch(j);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int64_t idx = threadIdx.x + 256 * t;
+            if (idx < MR * words) xs_pairs[idx] = pairs(d[t]);
+        }
+    } else {
+        for (int64_t idx = threadIdx.x; idx < MR * words; idx += 256) {
+            const int64_t m = idx / words, w = idx - m * words;
+            xs_pairs[idx] = pairs(ld16(x + (m < mr ? m : mr - 1) * K + 8 * w));
+        }
     }
     __syncthreads();
     for (int64_t idx = threadIdx.x; idx < MR * cpr; idx += 256) {
@@ -400,7 +427,7 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
         for (int m = 0; m < MR; ++m) acc[q][m] = 0.0f;
 
     for (int64_t base = j; base < cpr; base += 16 * QV_BATCH) {
-        load_batch(base);
+        if (!PF || base != j) load_batch(base);
 #pragma unroll
         for (int i = 0; i < QV_BATCH; ++i) {
             const int64_t c = base + 16 * i;
@@ -972,7 +999,12 @@ template <typename T, int EPI>
 int launch_qmv_dot2(const QParams &p, int mr, hipStream_t st) {
     const dim3 grid((unsigned)ceil_div(p.Nout, 16), (unsigned)ceil_div(p.M, mr));
     const size_t lds = (size_t)qmv_dot2_lds_bytes(mr, p.K);
-    if (mr == 1)
+    // weights requested under the x staging when the grid is at most four
+    // workgroups per CU (measured: N = 9728 gains, N = 151936 loses)
+    const bool pf = (int64_t)grid.x * grid.y <= 1024 && p.K / 8 <= 512;
+    if (mr == 1 && pf)
+        qmv_dot2_kernel<T, 1, EPI, true><<<grid, 256, lds, st>>>(p);
+    else if (mr == 1)
         qmv_dot2_kernel<T, 1, EPI><<<grid, 256, lds, st>>>(p);
     else if (mr == 2)
         qmv_dot2_kernel<T, 2, EPI><<<grid, 256, lds, st>>>(p);
