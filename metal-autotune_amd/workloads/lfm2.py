@@ -36,8 +36,8 @@ from dataclasses import dataclass, field
 import torch
 from torch import nn
 
-from autotuner_runtime import kernels as _kernels
 from autotuner_runtime import ops, regions
+from autotuner_runtime.serve import SizedRegions
 from autotuner_runtime.swap import ReplayWrapper, install
 
 from .qwen3 import KVCache, QuantizedEmbedding, QuantizedLinear, RMSNorm
@@ -213,27 +213,28 @@ def layer_specs(cfg: Lfm2Config, dtype: str = "bfloat16") -> dict:
     }
 
 
-def _mlp_regions(specs, mlp, hn, h):
+def _mlp_regions(wr, mlp, hn, h, n):
     w1, w3 = mlp.w1, mlp.w3
-    outs = _kernels.try_sized(specs["dual_swiglu"],
-                              [hn, w1.weight, w1.scales, w1.biases, w3.weight, w3.scales, w3.biases])
+    outs = wr._try("dual_swiglu",
+                   [hn, w1.weight, w1.scales, w1.biases, w3.weight, w3.scales, w3.biases], n)
     act = ops.swiglu(w1(hn), w3(hn)) if outs is None else outs[0]
     w2 = mlp.w2
-    outs = _kernels.try_sized(specs["residual"], [act, w2.weight, w2.scales, w2.biases, h])
+    outs = wr._try("residual", [act, w2.weight, w2.scales, w2.biases, h], n)
     return h + w2(act) if outs is None else outs[0]
 
 
-def _out_proj_regions(specs, proj, o, x, ffn_norm):
-    outs = _kernels.try_sized(specs["residual_rmsnorm"],
-                              [o, proj.weight, proj.scales, proj.biases, x, ffn_norm.weight])
+def _out_proj_regions(wr, proj, o, x, ffn_norm, n):
+    outs = wr._try("residual_rmsnorm",
+                   [o, proj.weight, proj.scales, proj.biases, x, ffn_norm.weight], n)
     if outs is None:
         h = x + proj(o)
         return h, ffn_norm(h)
     return outs[0], outs[1]
 
 
-class Lfm2ConvRegions(ReplayWrapper):
-    """The short-conv layer with the region cuts spliced in."""
+class Lfm2ConvRegions(SizedRegions):
+    """The short-conv layer with the region cuts spliced in (at the sizes each
+    kernel serves)."""
 
     KERNEL_IDS = ["lfm2_in_proj_split_gate", "lfm2_out_proj_add_norm", "lfm2_w1_w3_swiglu",
                   "lfm2_w2_add"]
@@ -243,9 +244,10 @@ class Lfm2ConvRegions(ReplayWrapper):
         if not (x.dim() == 3 and x.dtype == torch.bfloat16 and x.is_cuda):
             return w(x, cache)
         c = w.conv
+        L = x.shape[1]
         xn = w.operator_norm(x)
         p = c.in_proj
-        outs = _kernels.try_sized(self._specs["split_gate"], [xn, p.weight, p.scales, p.biases])
+        outs = self._try("split_gate", [xn, p.weight, p.scales, p.biases], L)
         if outs is None:
             y = p(xn)
             D = y.shape[-1] // 3
@@ -254,12 +256,13 @@ class Lfm2ConvRegions(ReplayWrapper):
             Cg, bx = outs
         D = bx.shape[-1]
         conv_out, cache.state = ops.shortconv(bx, Cg, c.conv.weight.reshape(D, 3), cache.state)
-        h, hn = _out_proj_regions(self._specs, c.out_proj, conv_out, x, w.ffn_norm)
-        return _mlp_regions(self._specs, w.feed_forward, hn, h)
+        h, hn = _out_proj_regions(self, c.out_proj, conv_out, x, w.ffn_norm, L)
+        return _mlp_regions(self, w.feed_forward, hn, h, L)
 
 
-class Lfm2AttnRegions(ReplayWrapper):
-    """The attention layer with the region cuts spliced in."""
+class Lfm2AttnRegions(SizedRegions):
+    """The attention layer with the region cuts spliced in (at the sizes each
+    kernel serves)."""
 
     KERNEL_IDS = ["lfm2_qkv_proj", "lfm2_out_proj_add_norm", "lfm2_w1_w3_swiglu", "lfm2_w2_add"]
 
@@ -272,8 +275,8 @@ class Lfm2AttnRegions(ReplayWrapper):
         B, L, _ = x.shape
         xn = w.operator_norm(x)
         projs = (a.q_proj, a.k_proj, a.v_proj)
-        outs = _kernels.try_sized(self._specs["qkv"],
-                                  [xn] + [t for m in projs for t in (m.weight, m.scales, m.biases)])
+        outs = self._try("qkv", [xn] + [t for m in projs for t in (m.weight, m.scales, m.biases)],
+                         L)
         q, k, v = (m(xn) for m in projs) if outs is None else outs
         qr = ops.norm_rope_qkv(q, k, v, a.q_layernorm.weight, a.k_layernorm.weight,
                                c.num_attention_heads, c.num_key_value_heads, c.norm_eps,
@@ -283,8 +286,8 @@ class Lfm2AttnRegions(ReplayWrapper):
                                              "causal" if L > 1 else None,
                                              kv_len=cache.offset + L,
                                              out_layout=1).reshape(B, L, -1)
-        h, hn = _out_proj_regions(self._specs, a.out_proj, o, x, w.ffn_norm)
-        return _mlp_regions(self._specs, w.feed_forward, hn, h)
+        h, hn = _out_proj_regions(self, a.out_proj, o, x, w.ffn_norm, L)
+        return _mlp_regions(self, w.feed_forward, hn, h, L)
 
 
 def install_regions(model: Lfm2Model) -> list:

@@ -32,9 +32,9 @@ from dataclasses import dataclass
 import torch
 from torch import nn
 
-from autotuner_runtime import kernels as _kernels
 from autotuner_runtime import ops, regions
-from autotuner_runtime.swap import ReplayWrapper, install
+from autotuner_runtime.serve import SizedRegions
+from autotuner_runtime.swap import install
 
 from .quantize import random_quantized
 
@@ -191,9 +191,10 @@ def layer_specs(cfg: Qwen3Config, dtype: str = "bfloat16") -> dict:
     }
 
 
-class Qwen3LayerRegions(ReplayWrapper):
-    """The decoder layer with the region cuts spliced in (try_sized, else the
-    original ops)."""
+class Qwen3LayerRegions(SizedRegions):
+    """The decoder layer with the region cuts spliced in (try_sized at the
+    sizes each kernel serves, else the original ops). A spec missing from the
+    table leaves its cut on the original ops."""
 
     KERNEL_IDS = ["qwen3_qkv_proj", "qwen3_o_proj_add_norm", "qwen3_gate_up_swiglu",
                   "qwen3_down_add"]
@@ -207,8 +208,8 @@ class Qwen3LayerRegions(ReplayWrapper):
         B, L, _ = x.shape
         xn = w.input_layernorm(x)
         projs = (attn.q_proj, attn.k_proj, attn.v_proj)
-        outs = _kernels.try_sized(self._specs["qkv"],
-                                  [xn] + [t for m in projs for t in (m.weight, m.scales, m.biases)])
+        outs = self._try("qkv", [xn] + [t for m in projs for t in (m.weight, m.scales, m.biases)],
+                         L)
         q, k, v = (m(xn) for m in projs) if outs is None else outs
         # q/k-norm + RoPE + the KV-cache update, one launch
         qr = ops.norm_rope_qkv(q, k, v, attn.q_norm.weight, attn.k_norm.weight,
@@ -220,19 +221,18 @@ class Qwen3LayerRegions(ReplayWrapper):
                                              kv_len=cache.offset + L,
                                              out_layout=1).reshape(B, L, -1)
         op, pn = attn.o_proj, w.post_attention_layernorm
-        outs = _kernels.try_sized(self._specs["residual_rmsnorm"],
-                                  [o, op.weight, op.scales, op.biases, x, pn.weight])
+        outs = self._try("residual_rmsnorm", [o, op.weight, op.scales, op.biases, x, pn.weight], L)
         if outs is None:
             h = x + op(o)
             hn = pn(h)
         else:
             h, hn = outs
         g, u = mlp.gate_proj, mlp.up_proj
-        outs = _kernels.try_sized(self._specs["dual_swiglu"],
-                                  [hn, g.weight, g.scales, g.biases, u.weight, u.scales, u.biases])
+        outs = self._try("dual_swiglu",
+                         [hn, g.weight, g.scales, g.biases, u.weight, u.scales, u.biases], L)
         act = ops.swiglu(g(hn), u(hn)) if outs is None else outs[0]
         d = mlp.down_proj
-        outs = _kernels.try_sized(self._specs["residual"], [act, d.weight, d.scales, d.biases, h])
+        outs = self._try("residual", [act, d.weight, d.scales, d.biases, h], L)
         return h + d(act) if outs is None else outs[0]
 
 
