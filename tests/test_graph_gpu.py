@@ -1,0 +1,83 @@
+"""Graph-level delivery: GraphWrapper captures a scope once per call
+signature as a HIP graph and replays it; outputs and cache state must equal
+the eager scope's bit for bit, on replays after the first too (with eager work
+and synchronisations in between)."""
+
+from __future__ import annotations
+
+import pytest
+
+torch = pytest.importorskip("torch")
+
+
+def test_signature_distinguishes_state_and_shapes():
+    from autotuner_runtime.graph import signature
+
+    class Cache:
+        def __init__(self, t, offset):
+            self.keys, self.offset = t, offset
+
+    t = torch.zeros(4, 8)
+    a = signature((torch.zeros(2, 3), Cache(t, 0)))
+    assert a == signature((torch.ones(2, 3), Cache(t, 0)))        # values do not matter
+    assert a != signature((torch.zeros(2, 4), Cache(t, 0)))       # shapes do
+    assert a != signature((torch.zeros(2, 3), Cache(t, 5)))       # plain state does
+    assert a != signature((torch.zeros(2, 3), Cache(t.clone(), 0)))  # and the buffer identity
+
+
+@pytest.mark.gpu
+@pytest.mark.timeout(600)
+def test_graph_wrapper_qwen3_prefill_replays_equal_eager():
+    from workloads import qwen3
+    from autotuner_runtime.graph import GraphWrapper
+
+    cfg = qwen3.Qwen3Config()
+    model = qwen3.build(cfg, seed=4, num_layers=2)
+    qwen3.install_regions(model)
+    gw = GraphWrapper(model, max_graphs=2)
+    caches_g, caches_e = model.make_cache(256), model.make_cache(256)
+    ids = [qwen3.tokens(s, 128, cfg.vocab_size) for s in (1, 2, 3)]
+    for i, t in enumerate(ids):
+        for c in caches_g + caches_e:
+            c.offset = 0
+        got = gw(t, caches_g).clone()
+        want = model(t, caches_e)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"call {i}"
+        assert all(cg.offset == 128 for cg in caches_g)
+        assert all(torch.equal(a.keys, b.keys) and torch.equal(a.values, b.values)
+                   for a, b in zip(caches_g, caches_e))
+        _ = torch.randn(1000, device="cuda").sum().item()  # eager work between replays
+    assert gw.stats == {"captures": 1, "replays": 2, "eager": 0}
+    # a new prompt length is a new signature; beyond max_graphs calls run eagerly
+    for L, kind in ((64, "captures"), (32, "eager")):
+        for c in caches_g + caches_e:
+            c.offset = 0
+        t = qwen3.tokens(9, L, cfg.vocab_size)
+        got, want = gw(t, caches_g).clone(), model(t, caches_e)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+    assert gw.stats == {"captures": 2, "replays": 2, "eager": 1}
+
+
+@pytest.mark.gpu
+def test_graph_wrapper_carries_conv_state():
+    """An LFM2 conv layer sets cache.state during its call: a replay hands the
+    caller the graph's state tensor, equal to the eager state."""
+    from workloads import lfm2
+    from autotuner_runtime.graph import GraphWrapper
+
+    cfg = lfm2.Lfm2Config()
+    model = lfm2.build(cfg, seed=6, num_layers=1, layer_types=("conv",))
+    layer = lfm2.Lfm2ConvRegions(model.model.layers[0], lfm2.layer_specs(cfg))
+    gw = GraphWrapper(layer)
+    for seed in (1, 2, 3):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        x = torch.randn((1, 96, cfg.hidden_size), generator=g, device="cuda").to(torch.bfloat16)
+        cg, ce = lfm2.ConvCache(), lfm2.ConvCache()
+        got = gw(x, cg).clone()
+        want = layer(x, ce)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want) and torch.equal(cg.state, ce.state)
+    assert gw.stats["captures"] == 1 and gw.stats["replays"] == 2
