@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MI_ABI_VERSION 1
+#define MI_ABI_VERSION 2  /* 2: mi_argmax takes a workspace */
 
 enum mi_dtype { MI_F32 = 0, MI_F16 = 1, MI_BF16 = 2 };
 
@@ -191,9 +191,17 @@ int mi_shortconv(const void *bx, const void *c, const void *w, const void *state
 int mi_linear_f32(const float *x, const float *w, const float *bias, float *y, int64_t M,
                   int64_t N, int64_t K, int act, void *stream);
 
-/* Greedy sampling (mlx-lm glue): out[r] = argmax over x[r, 0:V]; the lowest
- * index wins a tie; NaN never wins. out is int32 [rows]. */
-int mi_argmax(const void *x, int32_t *out, int64_t rows, int64_t V, int dtype, void *stream);
+/* Greedy sampling (mlx-lm glue; mx.argmax(logits, axis=-1) in mlx-lm's
+ * generate loop): out[r] = argmax over x[r, 0:V]; the lowest index wins a
+ * tie; NaN never wins; a row with no non-NaN value gives 0. out is int32
+ * [rows]; V < 2^31.
+ * workspace: device memory of at least mi_argmax_workspace_bytes(rows, V)
+ * bytes, 8-byte aligned, rows <= 65535; with it each row is split over many
+ * workgroups (two launches). NULL: one workgroup per row (one launch). Same
+ * result either way. Calls that share a workspace must not overlap. */
+int64_t mi_argmax_workspace_bytes(int64_t rows, int64_t V);
+int mi_argmax(const void *x, int32_t *out, int64_t rows, int64_t V, int dtype, void *workspace,
+              int64_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

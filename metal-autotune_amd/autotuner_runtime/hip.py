@@ -23,7 +23,7 @@ import torch
 
 PKG = Path(__file__).resolve().parent.parent
 LIB_PATH = Path(os.environ.get("MI_QMM_LIB", PKG / "libmiqmm.so"))
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 MI_F32, MI_F16, MI_BF16 = 0, 1, 2
 MI_OK, MI_ERR_ARG, MI_ERR_UNSUPPORTED, MI_ERR_LAUNCH = 0, 1, 2, 3
@@ -55,8 +55,10 @@ SIGNATURES: dict[str, list] = {
     "mi_swiglu": [_P, _P, _P, _I64, _I, _P],
     "mi_shortconv": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P],
     "mi_linear_f32": [_P, _P, _P, _P, _I64, _I64, _I64, _I, _P],
-    "mi_argmax": [_P, _P, _I64, _I64, _I, _P],
+    "mi_argmax_workspace_bytes": [_I64, _I64],
+    "mi_argmax": [_P, _P, _I64, _I64, _I, _P, _I64, _P],
 }
+RESTYPES = {"mi_last_error": ctypes.c_char_p, "mi_argmax_workspace_bytes": ctypes.c_int64}
 
 _lock = threading.Lock()
 _lib = None
@@ -81,7 +83,7 @@ def lib():
         for name, argtypes in SIGNATURES.items():
             fn = getattr(L, name)
             fn.argtypes = argtypes
-            fn.restype = ctypes.c_char_p if name == "mi_last_error" else ctypes.c_int
+            fn.restype = RESTYPES.get(name, ctypes.c_int)
         if L.mi_abi_version() != ABI_VERSION:
             raise RuntimeError(f"{LIB_PATH}: ABI {L.mi_abi_version()} != {ABI_VERSION}")
         _lib = L
@@ -402,7 +404,15 @@ def b_argmax(ins, outs, p):
     V = x.shape[-1]
     if o.dtype != torch.int32 or o.numel() != x.numel() // V:
         raise ValueError("argmax output must be int32 with one entry per row")
-    _check(lib().mi_argmax(_ptr(x), _ptr(o), x.numel() // V, V, _dt(x), _stream(x)), "argmax")
+    rows = x.numel() // V
+    # split path: a workspace from torch's allocator (graph-capture safe); the
+    # one-workgroup path (no workspace) when p["split"] is False
+    ws, nbytes = None, 0
+    if p.get("split", True) and 0 < rows <= 65535:
+        nbytes = int(lib().mi_argmax_workspace_bytes(rows, V))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    _check(lib().mi_argmax(_ptr(x), _ptr(o), rows, V, _dt(x), _ptr(ws), nbytes, _stream(x)),
+           "argmax")
 
 
 BINDINGS: dict[str, Callable] = {

@@ -243,11 +243,13 @@ def linear_f32(x, w, bias=None, gelu: bool = False) -> torch.Tensor:
     return y
 
 
-def argmax(x) -> torch.Tensor:
-    """Greedy token: argmax over the last axis (lowest index on ties) as int32."""
+def argmax(x, split: bool = True) -> torch.Tensor:
+    """Greedy token: argmax over the last axis (lowest index on ties) as int32.
+    split: each row over many workgroups (default) or one workgroup per row;
+    the result is the same."""
     x = x.contiguous()
     o = _empty(x.shape[:-1], x, torch.int32)
-    hip.b_argmax([x], [o], {})
+    hip.b_argmax([x], [o], {"split": split})
     return o
 
 

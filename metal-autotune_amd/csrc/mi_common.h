@@ -53,6 +53,14 @@ template <typename T> __device__ __forceinline__ uint4 pack8(const float (&f)[8]
     return __builtin_bit_cast(uint4, v);
 }
 
+// Two floats to the two T lanes of one dword (a low, b high), each rounded to
+// nearest even; bf16 pairs take one v_cvt_pk_bf16_f32.
+template <typename T> __device__ __forceinline__ uint32_t pk2(float a, float b) {
+    typedef float F2 __attribute__((ext_vector_type(2)));
+    typedef T T2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((F2){a, b}, T2));
+}
+
 template <typename T> __device__ __forceinline__ uint2 pack4(const float (&f)[4]) {
     typedef typename Vec<T>::x4 V;
     V v;
@@ -68,7 +76,10 @@ template <typename T> __device__ __forceinline__ uint2 pack4(const float (&f)[4]
 template <typename T, int BITS>
 __device__ __forceinline__ typename Vec<T>::x8 dequant8(uint32_t w0, uint32_t w1, float s,
                                                        float b) {
-    typename Vec<T>::x8 r;
+    // Values 2k and 2k + 1 are converted together (pk2): converted one by
+    // one, the compiler packed mismatched pairs and re-shuffled them, five
+    // extra VALU per 8 values.
+    uint32_t r[4];
     if constexpr (BITS == 4) {
         // even nibbles to the bytes of lo, odd nibbles to the bytes of hi, so
         // each value converts with one v_cvt_f32_ubyte{0..3}; the empty asm
@@ -77,18 +88,19 @@ __device__ __forceinline__ typename Vec<T>::x8 dequant8(uint32_t w0, uint32_t w1
         uint32_t lo = w0 & 0x0F0F0F0Fu, hi = (w0 >> 4) & 0x0F0F0F0Fu;
         asm("" : "+v"(lo), "+v"(hi));
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            r[2 * k] = (T)__builtin_fmaf(s, (float)((lo >> (8 * k)) & 255u), b);
-            r[2 * k + 1] = (T)__builtin_fmaf(s, (float)((hi >> (8 * k)) & 255u), b);
-        }
+        for (int k = 0; k < 4; ++k)
+            r[k] = pk2<T>(__builtin_fmaf(s, (float)((lo >> (8 * k)) & 255u), b),
+                          __builtin_fmaf(s, (float)((hi >> (8 * k)) & 255u), b));
     } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            r[i] = (T)__builtin_fmaf(s, (float)((w0 >> (8 * i)) & 255u), b);
-            r[4 + i] = (T)__builtin_fmaf(s, (float)((w1 >> (8 * i)) & 255u), b);
+        for (int k = 0; k < 2; ++k) {
+            r[k] = pk2<T>(__builtin_fmaf(s, (float)((w0 >> (16 * k)) & 255u), b),
+                          __builtin_fmaf(s, (float)((w0 >> (16 * k + 8)) & 255u), b));
+            r[2 + k] = pk2<T>(__builtin_fmaf(s, (float)((w1 >> (16 * k)) & 255u), b),
+                              __builtin_fmaf(s, (float)((w1 >> (16 * k + 8)) & 255u), b));
         }
     }
-    return r;
+    return __builtin_bit_cast(typename Vec<T>::x8, (uint4){r[0], r[1], r[2], r[3]});
 }
 
 // Register "launder": an empty asm that claims to rewrite the value. Placed

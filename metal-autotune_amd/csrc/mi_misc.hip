@@ -176,6 +176,100 @@ __global__ __launch_bounds__(AM_THREADS) void argmax_kernel(const T *__restrict_
     }
 }
 
+// Split argmax: a row is cut into spans of AM_SPAN units (16-byte chunks when
+// VEC, else single values); workgroup (g, row) reduces span g to one
+// (value, index) partial, then one wave per row merges the row's partials.
+// The merge is a total order (larger value, then lower index; NaN never
+// wins), so the result equals the one-workgroup kernel's.
+constexpr int AM_SPLIT_THREADS = 256;
+constexpr int AM_SPAN_CHUNKS = 2 * AM_SPLIT_THREADS;  // 16-byte chunks per workgroup
+constexpr int AM_SPAN_VALUES = 8 * AM_SPLIT_THREADS;  // values per workgroup (scalar path)
+
+struct AmPart {
+    float v;
+    int32_t i;  // -1: the span holds no non-NaN value
+};
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(AM_SPLIT_THREADS) void argmax_part_kernel(const T *__restrict__ x,
+                                                                        AmPart *__restrict__ part,
+                                                                        int64_t V) {
+    constexpr int E = 16 / (int)sizeof(T);
+    constexpr int NW = AM_SPLIT_THREADS / 64;
+    __shared__ float sv[NW];
+    __shared__ int32_t si[NW];
+    const T *row = x + (int64_t)blockIdx.y * V;
+    float best = -INFINITY;
+    int64_t bi = -1;
+    if constexpr (VEC) {
+        const int64_t nc = V / E;
+        const int64_t c0 = (int64_t)blockIdx.x * AM_SPAN_CHUNKS + threadIdx.x;
+        uint4 d[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int64_t c = c0 + u * AM_SPLIT_THREADS;
+            d[u] = ld16(row + (c < nc ? c : nc - 1) * E);  // clamped: always in bounds
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int64_t c = c0 + u * AM_SPLIT_THREADS;
+            if (c >= nc) break;
+            float f[E];
+            if constexpr (sizeof(T) == 2) {
+                unpack8<T>(d[u], f);
+            } else {
+                f[0] = __uint_as_float(d[u].x);
+                f[1] = __uint_as_float(d[u].y);
+                f[2] = __uint_as_float(d[u].z);
+                f[3] = __uint_as_float(d[u].w);
+            }
+#pragma unroll
+            for (int e = 0; e < E; ++e) am_take(f[e], c * E + e, best, bi);
+        }
+    } else {
+        const int64_t i0 = (int64_t)blockIdx.x * AM_SPAN_VALUES;
+        const int64_t i1 = i0 + AM_SPAN_VALUES < V ? i0 + AM_SPAN_VALUES : V;
+        for (int64_t i = i0 + threadIdx.x; i < i1; i += AM_SPLIT_THREADS)
+            am_take((float)row[i], i, best, bi);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int64_t oi = __shfl_xor(bi, o, 64);
+        am_merge(ov, oi, best, bi);
+    }
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sv[wave] = best;
+        si[wave] = (int32_t)bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w2 = 1; w2 < NW; ++w2) am_merge(sv[w2], si[w2], best, bi);
+        part[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = AmPart{best, (int32_t)bi};
+    }
+}
+
+__global__ __launch_bounds__(64) void argmax_merge_kernel(const AmPart *__restrict__ part, int G,
+                                                          int32_t *__restrict__ out) {
+    const AmPart *p = part + (int64_t)blockIdx.x * G;
+    float best = -INFINITY;
+    int64_t bi = -1;
+    for (int g = threadIdx.x; g < G; g += 64) am_merge(p[g].v, p[g].i, best, bi);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int64_t oi = __shfl_xor(bi, o, 64);
+        am_merge(ov, oi, best, bi);
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = (int32_t)(bi < 0 ? 0 : bi);
+}
+
+// spans per row of the split argmax
+int64_t am_spans(int64_t V, int esize, bool vec) {
+    return vec ? ceil_div(V * esize / 16, AM_SPAN_CHUNKS) : ceil_div(V, AM_SPAN_VALUES);
+}
+
 }  // namespace
 }  // namespace mi
 
@@ -240,21 +334,44 @@ extern "C" int mi_linear_f32(const float *x, const float *w, const float *bias, 
     return launch_status("linear_f32");
 }
 
+extern "C" int64_t mi_argmax_workspace_bytes(int64_t rows, int64_t V) {
+    if (rows <= 0 || V <= 0) return 0;
+    return rows * ceil_div(V, AM_SPAN_VALUES) * (int64_t)sizeof(AmPart);
+}
+
 extern "C" int mi_argmax(const void *x, int32_t *out, int64_t rows, int64_t V, int dtype,
-                         void *stream) {
+                         void *workspace, int64_t workspace_bytes, void *stream) {
     if (!valid_dtype(dtype)) return fail(MI_ERR_UNSUPPORTED, "dtype code %d", dtype);
     if (rows < 0 || V <= 0) return fail(MI_ERR_ARG, "argmax shape");
+    if (V > INT32_MAX) return fail(MI_ERR_ARG, "argmax row of %lld values exceeds int32", (long long)V);
     if (rows == 0) return MI_OK;
     if (!x || !out) return fail(MI_ERR_ARG, "null pointer");
+    if (workspace && workspace_bytes < mi_argmax_workspace_bytes(rows, V))
+        return fail(MI_ERR_ARG, "argmax workspace of %lld bytes, %lld needed",
+                    (long long)workspace_bytes, (long long)mi_argmax_workspace_bytes(rows, V));
+    if (workspace && !aligned(workspace, 8)) return fail(MI_ERR_ARG, "argmax workspace alignment");
+    if (workspace && rows > 65535) return fail(MI_ERR_ARG, "argmax: more than 65535 rows");
     hipStream_t st = as_stream(stream);
     const int esize = dtype == MI_F32 ? 4 : 2;
     const bool vec = aligned(x, 16) && (V * esize) % 16 == 0;
+    const int64_t G = am_spans(V, esize, vec);
+    AmPart *part = (AmPart *)workspace;
 #define MI_AM(TT)                                                                               \
     do {                                                                                        \
-        if (vec)                                                                                \
+        if (part) {                                                                             \
+            const dim3 grid((unsigned)G, (unsigned)rows);                                       \
+            if (vec)                                                                            \
+                argmax_part_kernel<TT, true><<<grid, AM_SPLIT_THREADS, 0, st>>>((const TT *)x,  \
+                                                                               part, V);       \
+            else                                                                                \
+                argmax_part_kernel<TT, false><<<grid, AM_SPLIT_THREADS, 0, st>>>((const TT *)x, \
+                                                                                part, V);      \
+            argmax_merge_kernel<<<(unsigned)rows, 64, 0, st>>>(part, (int)G, out);             \
+        } else if (vec) {                                                                       \
             argmax_kernel<TT, true><<<(unsigned)rows, AM_THREADS, 0, st>>>((const TT *)x, out, V); \
-        else                                                                                    \
+        } else {                                                                                \
             argmax_kernel<TT, false><<<(unsigned)rows, AM_THREADS, 0, st>>>((const TT *)x, out, V); \
+        }                                                                                       \
     } while (0)
     if (dtype == MI_BF16)
         MI_AM(bf16);

@@ -554,8 +554,12 @@ struct MfmaShape {
     // vmcnt at the top of a stage: the loads of the PIPE - 2 stages issued
     // after it may still be in flight (vmcnt decrements in issue order)
     static constexpr int VMCNT = (PIPE - 2) * OPS;
+    // vmcnt once the ring prologue (PIPE - 1 stages of DMAs, plus the first
+    // stage's register weights) is issued: only the scale/bias table before it
+    // has landed
+    static constexpr int TABLE_VMCNT = (PIPE - 1) * OPS + (WREG ? A * SPS : 0);
     static_assert(WK % WF == 0 && (ROWS / 8) % WF == 0, "x instructions split evenly");
-    static_assert(PIPE >= 2 && PIPE <= MAX_PIPE && VMCNT < 64, "vmcnt is a 6-bit count");
+    static_assert(PIPE >= 2 && PIPE <= MAX_PIPE && TABLE_VMCNT < 64, "vmcnt is a 6-bit count");
     static_assert(!WREG || PIPE == 2, "register-prefetched weights run one stage ahead");
     static_assert(LDS <= LDS_PER_CU, "stage rings exceed the LDS of a CU");
 };
@@ -703,15 +707,20 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
     const int sbrow = (r * pitch + hg - gbase) * 2;
     // x DMA: instruction i writes stage rows 8i..8i+7; lane l fills row
     // 8i + l/8 at swizzled position l%8, i.e. it loads chunk (l%8) ^ swz(row).
-    // Wave fw issues instructions i = WF * j + fw.
-    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(p.x, (uint32_t)(p.M * K * (int64_t)sizeof(T)));
+    // Wave fw issues instructions i = WF * j + fw. Tokens past M point past
+    // the end of x's buffer resource: the load returns zeros without a memory
+    // access, and every lane still issues the same instructions (the end
+    // offset plus a stage offset stays below 2^32 since M * K * size < 2^31).
+    const uint32_t xbytes = (uint32_t)(p.M * K * (int64_t)sizeof(T));
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(p.x, xbytes);
     uint32_t xoff[Sh::XOPS];
 #pragma unroll
     for (int j = 0; j < Sh::XOPS; ++j) {
         const int row = 8 * (WF * j + fw) + (lane >> 3);
-        const int64_t m = m_blk + row < p.M ? m_blk + row : p.M - 1;
         const int chunk = (lane & 7) ^ ((row >> 1) & 7);
-        xoff[j] = (uint32_t)((m * K + 8 * chunk) * (int64_t)sizeof(T));
+        xoff[j] = m_blk + row < p.M
+                      ? (uint32_t)(((m_blk + row) * K + 8 * chunk) * (int64_t)sizeof(T))
+                      : xbytes;
     }
     auto issue = [&](int st, char *slot) {
         const int k0 = kbeg + st * XK;
@@ -788,9 +797,26 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
                : j == 6 ? b6 : b7;
     };
     const int last = nst > 0 ? nst - 1 : 0;
+    // Scales and biases of a stage are read from the table one stage ahead,
+    // so a stage's first dequant waits only for its weight chunk, not for the
+    // x fragments read before it (LDS reads complete in order).
+    uint32_t sq[A][SPS], bq[A][SPS];
+    auto load_sb = [&](int st) {
+#pragma unroll
+        for (int a = 0; a < A; ++a)
+#pragma unroll
+            for (int u = 0; u < SPS; ++u) {
+                const char *sb = tb + 2 * a * tab + sbrow + ((kbeg + st * XK + u * SS) >> gshift) * 2;
+                sq[a][u] = *(const uint16_t *)sb;
+                bq[a][u] = *(const uint16_t *)(sb + tab);
+            }
+    };
 #pragma unroll
     for (int j = 0; j < PIPE - 1; ++j) issue(j < last ? j : last, ring(j));
     if constexpr (Sh::WREG) load_w(0, wreg[0]);
+    // the table's DMAs were issued before the ring prologue's
+    wait_vmcnt<Sh::TABLE_VMCNT>();
+    load_sb(0);
     for (int st0 = 0; st0 < nst; st0 += PIPE) {
 #pragma unroll
         for (int j = 0; j < PIPE; ++j) {
@@ -799,6 +825,19 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
             wait_vmcnt<Sh::VMCNT>();
             if constexpr (WF > 1) stage_barrier();
             const char *cur = ring(j);
+            // the weight chunk first: the first dequant needs it, while the
+            // MFMAs that consume the x fragments come after that dequant
+            uint4 wq[A][SPS];
+#pragma unroll
+            for (int a = 0; a < A; ++a)
+#pragma unroll
+                for (int u = 0; u < SPS; ++u) {
+                    if constexpr (Sh::WREG)
+                        wq[a][u] = wreg[j][a][u];
+                    else
+                        wq[a][u] = *(const uint4 *)(cur + wslot + (a * SPS + u) * 1024 + lane * 16);
+                }
+            __builtin_amdgcn_sched_barrier(0);
             uint4 xf[C][SPS][S];
 #pragma unroll
             for (int c = 0; c < C; ++c)
@@ -810,21 +849,6 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
                         xf[c][u][s] =
                             *(const uint4 *)(cur + (32 * c + r) * 128 + ((chunk ^ swz) << 4));
                     }
-            uint4 wq[A][SPS];
-            uint32_t sq[A][SPS], bq[A][SPS];
-#pragma unroll
-            for (int a = 0; a < A; ++a)
-#pragma unroll
-                for (int u = 0; u < SPS; ++u) {
-                    if constexpr (Sh::WREG)
-                        wq[a][u] = wreg[j][a][u];
-                    else
-                        wq[a][u] = *(const uint4 *)(cur + wslot + (a * SPS + u) * 1024 + lane * 16);
-                    const char *sb = tb + 2 * a * tab + sbrow +
-                                     ((kbeg + st * XK + u * SS) >> gshift) * 2;
-                    sq[a][u] = *(const uint16_t *)sb;
-                    bq[a][u] = *(const uint16_t *)(sb + tab);
-                }
             const int nx = st + PIPE - 1 < last ? st + PIPE - 1 : last;
             issue(nx, ring((j + PIPE - 1) % PIPE));
             if constexpr (Sh::WREG) {  // PIPE == 2: the next stage, into the other set
@@ -849,6 +873,7 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
                                 Mfma<T>::mma(af, __builtin_bit_cast(V8, xf[c][u][s]), acc[a][c]);
                     }
             __builtin_amdgcn_sched_barrier(0);
+            load_sb(st < last ? st + 1 : last);
         }
     }
     };

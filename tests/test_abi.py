@@ -42,8 +42,17 @@ def test_library_exports_every_declared_symbol(lib):
 def test_abi_version_and_error_string(lib):
     lib.mi_abi_version.restype = ctypes.c_int
     lib.mi_last_error.restype = ctypes.c_char_p
-    assert lib.mi_abi_version() == 1
+    assert lib.mi_abi_version() == 2
     assert isinstance(lib.mi_last_error(), bytes)
+
+
+def test_argmax_workspace_query_needs_no_device(lib):
+    """The workspace bound: 8 bytes per 2048-value span per row."""
+    lib.mi_argmax_workspace_bytes.restype = ctypes.c_int64
+    lib.mi_argmax_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_int64]
+    assert lib.mi_argmax_workspace_bytes(1, 151936) == 600
+    assert lib.mi_argmax_workspace_bytes(4, 2049) == 64
+    assert lib.mi_argmax_workspace_bytes(0, 10) == 0
 
 
 def test_argument_errors_need_no_device(lib):

@@ -382,22 +382,28 @@ def test_linear_gelu_f32():
     _close(h, want, "float32", 1e-5)
 
 
+@pytest.mark.parametrize("split", [True, False])
 @pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
-def test_argmax_lowest_index_on_ties(dtype):
+def test_argmax_lowest_index_on_ties(dtype, split):
+    """Ties across workgroup spans (4096 bf16 / 2048 f32 values per span on the
+    split path) and across threads: the lowest index wins; NaN never wins."""
     r = rng(1500)
-    x = oracle.round_to(r.normal(0, 1, (3, 151936)), dtype)
-    x[1, 77] = x[1, 90000] = 50.0          # tie: lowest index wins
+    x = oracle.round_to(r.normal(0, 1, (6, 151936)), dtype)
+    x[1, 77] = x[1, 90000] = 50.0          # tie across spans
     x[2, :] = -1.0
     x[2, 5] = float("nan")                  # NaN never wins
-    got = ops.argmax(to_torch(x, dtype)).cpu().numpy()
-    assert got[0] == int(np.argmax(x[0]))
-    assert got[1] == 77
-    assert got[2] == 0
+    x[3, 4095] = x[3, 4096] = x[3, 2047] = 60.0  # ties at span edges: 2047 wins
+    x[4, -1] = 70.0                         # maximum in the last element
+    x[5, :2048] = np.nan                    # a whole NaN span, maximum after it
+    x[5, 3000] = 80.0
+    got = ops.argmax(to_torch(x, dtype), split=split).cpu().numpy()
+    assert got.tolist() == [int(np.argmax(x[0])), 77, 0, 2047, 151935, 3000]
 
 
+@pytest.mark.parametrize("split", [True, False])
 @pytest.mark.parametrize("V", [1, 7, 1001, 8 * 1024 * 8 + 8, 65536])
 @pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
-def test_argmax_shapes_ties_nan_and_unaligned_rows(V, dtype):
+def test_argmax_shapes_ties_nan_and_unaligned_rows(V, dtype, split):
     """Vector (16-byte chunks) and scalar paths: random rows, a tie placed in
     one thread's later chunk and another thread's earlier one, an all-NaN row
     (-> 0), an all -inf row (-> 0), and a misaligned view (scalar path)."""
@@ -409,10 +415,28 @@ def test_argmax_shapes_ties_nan_and_unaligned_rows(V, dtype):
     x[3, :] = -np.inf
     want = [int(np.argmax(x[0])), 9 if V > 16 else int(np.argmax(x[1])), 0, 0,
             int(np.argmax(x[4]))]
-    got = ops.argmax(to_torch(x, dtype)).cpu().numpy()
+    got = ops.argmax(to_torch(x, dtype), split=split).cpu().numpy()
     assert got.tolist() == want
     flat = to_torch(np.concatenate([[0.0], x[4]]).astype(np.float32), dtype)
-    assert int(ops.argmax(flat[1:].reshape(1, V)).item()) == want[4]  # data_ptr + 1 element
+    assert int(ops.argmax(flat[1:].reshape(1, V), split=split).item()) == want[4]  # data_ptr + 1
+
+
+def test_argmax_workspace_size_and_checks():
+    """Workspace bytes: 8 per 2048-value span per row (a bound for every
+    path); a short or misaligned workspace is rejected before any launch."""
+    from autotuner_runtime import hip
+
+    L = hip.lib()
+    assert L.mi_argmax_workspace_bytes(1, 151936) == 8 * 75
+    assert L.mi_argmax_workspace_bytes(3, 2048) == 24 and L.mi_argmax_workspace_bytes(0, 5) == 0
+    x = torch.zeros((2, 4096), dtype=torch.bfloat16, device="cuda")
+    o = torch.empty(2, dtype=torch.int32, device="cuda")
+    ws = torch.empty(64, dtype=torch.uint8, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    assert L.mi_argmax(x.data_ptr(), o.data_ptr(), 2, 4096, hip.MI_BF16, ws.data_ptr(), 8, st) \
+        == hip.MI_ERR_ARG
+    assert L.mi_argmax(x.data_ptr(), o.data_ptr(), 2, 4096, hip.MI_BF16, ws.data_ptr() + 4, 60,
+                       st) == hip.MI_ERR_ARG
 
 
 def test_determinism_three_runs():
