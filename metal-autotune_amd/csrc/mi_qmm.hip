@@ -546,21 +546,34 @@ struct MfmaShape {
     static constexpr int WAVE = WREG ? 0 : A * SPS * 1024;           // a wave's weight chunks
     static constexpr int STAGE = XST + WF * WAVE;                    // one ring slot
     static constexpr int XBYTES = KG * PIPE * STAGE;                 // stage rings
-    static constexpr int RBYTES = (KG - 1) * WF * A * C * 16 * 64 * 4;  // K-split reduction
+    // PIPE == 1: one slot per wave; a stage reads its slot into registers,
+    // then the next stage's DMAs refill it (LEAD: stages issued ahead)
+    static constexpr bool SINGLE = PIPE == 1;
+    static constexpr int LEAD = SINGLE ? 1 : PIPE - 1;
+    // K-split reduction: the partial tiles of K-groups 1..KG-1 pass through
+    // the ring's LDS, RSLOTS at a time
+    static constexpr int PB = WF * A * C * 16 * 64 * 4;              // one K-group's partials
+    static constexpr int RSLOTS = KG <= 1 ? 1 : (XBYTES / PB >= KG - 1 ? KG - 1
+                                                 : (XBYTES / PB > 0 ? XBYTES / PB : 1));
+    static constexpr int RBYTES = RSLOTS * PB;
     static constexpr int LDS = XBYTES > RBYTES ? XBYTES : RBYTES;
     // DMA instructions a lane issues per stage: its share of x, and weights
     static constexpr int XOPS = ROWS / 8 / WF;
     static constexpr int OPS = XOPS + (WREG ? 0 : A * SPS);
-    // vmcnt at the top of a stage: the loads of the PIPE - 2 stages issued
+    // vmcnt at the top of a stage: the loads of the LEAD - 1 stages issued
     // after it may still be in flight (vmcnt decrements in issue order)
-    static constexpr int VMCNT = (PIPE - 2) * OPS;
-    // vmcnt once the ring prologue (PIPE - 1 stages of DMAs, plus the first
+    static constexpr int VMCNT = (LEAD - 1) * OPS;
+    // vmcnt once the ring prologue (LEAD stages of DMAs, plus the first
     // stage's register weights) is issued: only the scale/bias table before it
     // has landed
-    static constexpr int TABLE_VMCNT = (PIPE - 1) * OPS + (WREG ? A * SPS : 0);
+    static constexpr int TABLE_VMCNT = LEAD * OPS + (WREG ? A * SPS : 0);
+    // the stage loop is unrolled so ring slots and the two register weight
+    // sets are named statically
+    static constexpr int UNROLL = PIPE < 2 ? 2 : PIPE;
     static_assert(WK % WF == 0 && (ROWS / 8) % WF == 0, "x instructions split evenly");
-    static_assert(PIPE >= 2 && PIPE <= MAX_PIPE && TABLE_VMCNT < 64, "vmcnt is a 6-bit count");
-    static_assert(!WREG || PIPE == 2, "register-prefetched weights run one stage ahead");
+    static_assert(PIPE >= 1 && PIPE <= MAX_PIPE && TABLE_VMCNT < 64, "vmcnt is a 6-bit count");
+    static_assert(!WREG || PIPE <= 2, "register-prefetched weights run one stage ahead");
+    static_assert(!SINGLE || WF == 1, "a shared single slot would need a barrier before its refill");
     static_assert(LDS <= LDS_PER_CU, "stage rings exceed the LDS of a CU");
 };
 
@@ -591,16 +604,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, 
                                              0x00020000);
 }
 
-// Stages in flight per wave: the deepest ring (at most MI_QMM_MAX_PIPE, a
-// build-time tuning knob) whose four waves' slots fit the LDS of a CU.
-// Measured on MI355X at the Qwen3 prefill shapes, two stages win: a third
-// stage buys less than the second resident workgroup per CU it costs (two
-// waves per SIMD overlap one wave's dequant VALU with the other's MFMAs).
+// Ring slots per wave (MI_QMM_MAX_PIPE, a build-time tuning knob). Measured
+// on MI355X at the Qwen3 prefill shapes (M = 128), one slot wins: it halves
+// the ring, so three workgroups share a CU (three waves per SIMD, which
+// overlap one wave's dequant VALU with the others' MFMAs and loads), where
+// two slots allowed two workgroups and three slots one. Dual 38.0 -> 32.9 us,
+// q/k/v 15.0 -> 13.8, o_proj 12.1 -> 11.5, bit for bit the same results.
+// Above one, the deepest ring whose four waves' slots fit the LDS of a CU.
 #ifndef MI_QMM_MAX_PIPE
-#define MI_QMM_MAX_PIPE 2
+#define MI_QMM_MAX_PIPE 1
 #endif
 template <typename T, int BITS, int A, int C> constexpr int mfma_pipe() {
     typedef MfmaShape<T, BITS, A, C, 4, 2, 1> Sh2;
+    if constexpr (MI_QMM_MAX_PIPE <= 1) return 1;
     if constexpr (Sh2::WREG) return 2;
     constexpr int slot = Sh2::STAGE;
     constexpr int fit = 4 * 4 * slot <= LDS_PER_CU ? 4 : (4 * 3 * slot <= LDS_PER_CU ? 3 : 2);
@@ -614,6 +630,11 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// s_waitcnt lgkmcnt(0) with no wait on vmcnt (63) or expcnt (7)
+__device__ __forceinline__ void wait_lgkmcnt0() {
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
+}
+
 // Workgroup barrier with no memory fence: the waves have already waited for
 // their own DMAs into the stage (vmcnt), and LDS is one store per CU, so the
 // barrier alone makes the whole stage visible. (__syncthreads' fences would
@@ -625,8 +646,19 @@ __device__ __forceinline__ void stage_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// Waves per SIMD the register allocation must allow: the single-slot ring
+// exists so three workgroups of four waves share a CU (at most 168 registers
+// a lane), which tiles of up to four 32x32 accumulators fit without spilling;
+// larger tiles, and 128-token tiles (whose slot alone leaves room for two
+// workgroups), ask for two (256 registers).
+template <int PIPE, int A, int C> constexpr int mfma_waves_per_eu() {
+    return PIPE == 1 ? (A * C <= 4 && C <= 2 ? 3 : 2) : 1;
+}
+
 template <typename T, int BITS, int A, int C, int WK, int PIPE, int EPI, int WF = 1>
-__global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
+__global__ __launch_bounds__(64 * WK)
+__attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<PIPE, A, C>()))) void qmm_mfma_kernel(
+    QParams p) {
     // The body uses gfx950 buffer resources, which the host target cannot
     // type; the host pass needs only the launch stub.
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -774,11 +806,13 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
     // st + PIPE - 1 fill ring slot (st + PIPE - 1) % PIPE, which was last read
     // by stage st - 1 (its ds_reads completed before its MFMAs; with WF > 1
     // the barrier at the top of stage st also waits for the other waves to
-    // finish stage st - 1). Every stage issues exactly OPS DMAs -- past the
-    // last stage they re-read stage nst - 1, in bounds, into slots no later
-    // stage reads -- so at the top of stage st at most the loads of the
-    // PIPE - 2 stages after it are in flight: vmcnt(VMCNT). The stage loop is
-    // unrolled PIPE times so each slot is named statically.
+    // finish stage st - 1). PIPE == 1: one slot; stage st reads it into
+    // registers, waits for those reads, then refills it with stage st + 1.
+    // Every stage issues exactly OPS DMAs -- past the last stage they re-read
+    // stage nst - 1, in bounds, into slots no later stage reads -- so at the
+    // top of stage st at most the loads of the LEAD - 1 stages after it are in
+    // flight: vmcnt(VMCNT). The stage loop is unrolled (UNROLL) so each slot
+    // and register weight set is named statically.
     //
     // The slots (and the scale/bias table) are passed as separate __restrict__
     // arguments of the inlined main loop: the resulting alias scopes let the
@@ -812,19 +846,19 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
             }
     };
 #pragma unroll
-    for (int j = 0; j < PIPE - 1; ++j) issue(j < last ? j : last, ring(j));
+    for (int j = 0; j < Sh::LEAD; ++j) issue(j < last ? j : last, ring(j % PIPE));
     if constexpr (Sh::WREG) load_w(0, wreg[0]);
     // the table's DMAs were issued before the ring prologue's
     wait_vmcnt<Sh::TABLE_VMCNT>();
     load_sb(0);
-    for (int st0 = 0; st0 < nst; st0 += PIPE) {
+    for (int st0 = 0; st0 < nst; st0 += Sh::UNROLL) {
 #pragma unroll
-        for (int j = 0; j < PIPE; ++j) {
+        for (int j = 0; j < Sh::UNROLL; ++j) {
             const int st = st0 + j;
             if (st >= nst) break;  // workgroup-uniform
             wait_vmcnt<Sh::VMCNT>();
             if constexpr (WF > 1) stage_barrier();
-            const char *cur = ring(j);
+            const char *cur = ring(j % PIPE);
             // the weight chunk first: the first dequant needs it, while the
             // MFMAs that consume the x fragments come after that dequant
             uint4 wq[A][SPS];
@@ -833,7 +867,7 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
 #pragma unroll
                 for (int u = 0; u < SPS; ++u) {
                     if constexpr (Sh::WREG)
-                        wq[a][u] = wreg[j][a][u];
+                        wq[a][u] = wreg[j % 2][a][u];
                     else
                         wq[a][u] = *(const uint4 *)(cur + wslot + (a * SPS + u) * 1024 + lane * 16);
                 }
@@ -849,9 +883,16 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
                         xf[c][u][s] =
                             *(const uint4 *)(cur + (32 * c + r) * 128 + ((chunk ^ swz) << 4));
                     }
-            const int nx = st + PIPE - 1 < last ? st + PIPE - 1 : last;
-            issue(nx, ring((j + PIPE - 1) % PIPE));
-            if constexpr (Sh::WREG) {  // PIPE == 2: the next stage, into the other set
+            const int nx = st + Sh::LEAD < last ? st + Sh::LEAD : last;
+            if constexpr (Sh::SINGLE) {
+                // the slot's reads have returned before its refill is issued
+                __builtin_amdgcn_sched_barrier(0);
+                wait_lgkmcnt0();
+                issue(nx, ring(0));
+            } else {
+                issue(nx, ring((j + PIPE - 1) % PIPE));
+            }
+            if constexpr (Sh::WREG) {  // one stage ahead, into the other set
                 load_w(nx, wreg[(j + 1) % 2]);
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -887,14 +928,17 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
     wait_vmcnt<0>();
 
     if constexpr (Sh::KG > 1) {
-        // fixed-order reduction of the K-split partial tiles; the LDS staging
-        // is reused, so every wave must be done with its x stages first
+        // Fixed-order reduction of the K-split partial tiles: K-group 0 adds
+        // groups 1, 2, ... in turn. The ring's LDS is reused, RSLOTS partials
+        // per round, so every wave must be done with its x stages first; all
+        // waves take part in every round's barriers.
         constexpr int REGS = A * C * 16;
         float *red = (float *)lds;
         __syncthreads();
-        if (wk > 1) {
-            if (kw > 0) {
-                float *dst = red + (size_t)((kw - 1) * WF + fw) * REGS * 64 + lane;
+        for (int r0 = 1; r0 < wk; r0 += Sh::RSLOTS) {  // workgroup-uniform
+            const int r1 = r0 + Sh::RSLOTS < wk ? r0 + Sh::RSLOTS : wk;
+            if (kw >= r0 && kw < r1) {
+                float *dst = red + (size_t)((kw - r0) * WF + fw) * REGS * 64 + lane;
 #pragma unroll
                 for (int a = 0; a < A; ++a)
 #pragma unroll
@@ -903,17 +947,20 @@ __global__ __launch_bounds__(64 * WK) void qmm_mfma_kernel(QParams p) {
                         for (int i = 0; i < 16; ++i) dst[((a * C + c) * 16 + i) * 64] = acc[a][c][i];
             }
             __syncthreads();
-            if (kw > 0) return;
-            for (int src = 1; src < wk; ++src) {
-                const float *sp = red + (size_t)((src - 1) * WF + fw) * REGS * 64 + lane;
+            if (kw == 0) {
+                for (int src = r0; src < r1; ++src) {
+                    const float *sp = red + (size_t)((src - r0) * WF + fw) * REGS * 64 + lane;
 #pragma unroll
-                for (int a = 0; a < A; ++a)
+                    for (int a = 0; a < A; ++a)
 #pragma unroll
-                    for (int c = 0; c < C; ++c)
+                        for (int c = 0; c < C; ++c)
 #pragma unroll
-                        for (int i = 0; i < 16; ++i) acc[a][c][i] += sp[((a * C + c) * 16 + i) * 64];
+                            for (int i = 0; i < 16; ++i) acc[a][c][i] += sp[((a * C + c) * 16 + i) * 64];
+                }
             }
+            if (r1 < wk) __syncthreads();  // the slots are refilled next round
         }
+        if (kw > 0) return;
     }
 
     // D[row][col] of a 32x32 tile: col = lane % 32 (token), row = 8*(i/4) +
@@ -1013,8 +1060,14 @@ int launch_mfma(const QParams &p, hipStream_t st) {
             return launch_mfma_cfg<T, BITS, AL, 4, EPI>(p, wk, st);
     }
     if (p.M > 32 && nt * ceil_div(p.M, 64) >= 128 &&
-        mfma_lds_bytes<T, BITS, P, 2>(p, wk) <= LDS_PER_CU)
-        return launch_mfma_cfg<T, BITS, P, 2, EPI>(p, wk, st);
+        mfma_lds_bytes<T, BITS, P, 2>(p, wk) <= LDS_PER_CU) {
+        // 32-token tiles instead when the 64-token tile's LDS (its scale/bias
+        // tables grow with K) leaves fewer than three workgroups per CU and
+        // the 32-token tile's does not (down_proj, K = 9728: 25.4 -> 23.2 us)
+        const bool c1 = 3 * mfma_lds_bytes<T, BITS, P, 2>(p, wk) > LDS_PER_CU &&
+                        3 * mfma_lds_bytes<T, BITS, P, 1>(p, wk) <= LDS_PER_CU;
+        if (!c1) return launch_mfma_cfg<T, BITS, P, 2, EPI>(p, wk, st);
+    }
     if (mfma_lds_bytes<T, BITS, P, 1>(p, wk) <= LDS_PER_CU)
         return launch_mfma_cfg<T, BITS, P, 1, EPI>(p, wk, st);
     return launch_qmv<T, BITS, EPI>(p, st);
