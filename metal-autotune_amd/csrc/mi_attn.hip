@@ -1,21 +1,29 @@
 // Row A7: causal GQA scaled-dot-product attention (mx.fast.scaled_dot_product_attention
-// with mask='causal' or none), flash-style with 32-key tiles staged in LDS.
+// with mask='causal' or none), flash-style over 32-key tiles.
 //
-// A workgroup is 4 waves = 4 query heads that share one kv head (GQA: kv head
-// of q head h is h / (H/HK), tests/test_graph_model_matrix.py:84-93), all on
-// the same 32-query block, so each K/V tile is read from HBM once per group.
+// A workgroup is one query head (GQA: kv head of q head h is h / (H/HK),
+// tests/test_graph_model_matrix.py:84-93) on one 32-query block. Its 4 waves
+// split the block's key tiles: wave w takes tiles w, w + 4, w + 8, ... and
+// keeps its own online-softmax state; the 4 partial states are merged at the
+// end in LDS, in wave order. (A prefill of 128 tokens has 4 key tiles for its
+// last block: one per wave, and 32 heads x 4 blocks = 128 workgroups.)
 // Per wave and tile:
-//   S^T[key][q] = K . Q^T   32x32x16 MFMA, A = K rows from LDS, B = Q^T held
-//                           in registers for the whole kernel;
+//   S^T[key][q] = K . Q^T   32x32x16 MFMA, A = K rows loaded straight into
+//                           registers (16 bytes per lane and k-step), B = Q^T
+//                           held in registers for the whole kernel;
 //   lane (q = lane%32, half) then holds 16 of the 32 keys of its query row, so
 //   the row max/sum needs one xor-32 shuffle;
-//   O^T[d][q] += V^T . P^T  A = V^T from a transposed LDS tile, B = P^T
-//                           straight from the S^T registers (bf16/fp16): the
-//                           k order inside each MFMA is permuted to match the
-//                           S^T register layout, for both operands.
+//   O^T[d][q] += V^T . P^T  A = V^T from the wave's own transposed LDS tile,
+//                           B = P^T straight from the S^T registers (bf16/fp16):
+//                           the k order inside each MFMA is permuted to match
+//                           the S^T register layout, for both operands.
 // Online softmax in the log2 domain, fp32 running max/sum, one division at
 // the end. Causal masking is bottom-right aligned (query i sees keys
 // j <= i + Lk - Lq) and key tiles past the last visible key are skipped.
+// A query row's result depends only on its global position and the keys'
+// (tiles of 32 from key 0, dealt to waves by tile index), so a chunked
+// prefill whose chunks start at multiples of 32 reproduces the whole prefill
+// bit for bit.
 #include <math.h>
 
 #include "mi_common.h"
@@ -35,39 +43,46 @@ template <> struct AMfma<f16> {
     }
 };
 
+constexpr int ATT_WAVES = 4;  // key-tile splits per workgroup
+
+// LDS of one workgroup: the waves' V^T tiles, reused afterwards for the
+// partial states of waves 1..3 (o: DT x 16 floats per lane; l, m per lane).
+template <int D> struct AttnLds {
+    static constexpr int KT = 32;
+    static constexpr int VP = KT + 8;  // padded V^T-tile row (elements)
+    static constexpr int DT = D / 32;
+    static constexpr int VT_BYTES = D * VP * 2;                           // one wave's V^T tile
+    static constexpr int PART_FLOATS = DT * 16 * 64 + 2 * 64;             // one wave's state
+    static constexpr int BYTES = ATT_WAVES * VT_BYTES > (ATT_WAVES - 1) * PART_FLOATS * 4
+                                     ? ATT_WAVES * VT_BYTES
+                                     : (ATT_WAVES - 1) * PART_FLOATS * 4;
+};
+
 template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_kernel(const T *__restrict__ q,
-                                                   const T *__restrict__ k,
-                                                   const T *__restrict__ v, T *__restrict__ out,
-                                                   int64_t H, int64_t HK, int64_t Lq, int64_t Lk,
-                                                   int64_t cap, float scale_log2, int causal,
-                                                   int out_layout, int quads) {
-    constexpr int KT = 32;      // keys per tile
-    constexpr int KP = D + 8;   // padded K-tile row (elements)
-    constexpr int VP = KT + 8;  // padded V^T-tile row (elements)
+__global__ __launch_bounds__(64 * ATT_WAVES) void attn_kernel(
+    const T *__restrict__ q, const T *__restrict__ k, const T *__restrict__ v,
+    T *__restrict__ out, int64_t H, int64_t HK, int64_t Lq, int64_t Lk, int64_t cap,
+    float scale_log2, int causal, int out_layout) {
+    typedef AttnLds<D> L;
+    constexpr int KT = L::KT, VP = L::VP, DT = L::DT;
     constexpr int DS = D / 16;  // MFMA k-steps over the head dim
-    constexpr int DT = D / 32;  // 32-wide output tiles over the head dim
     typedef typename Vec<T>::x8 V8;
     typedef typename Vec<T>::x4 V4;
-    __shared__ __attribute__((aligned(16))) T ks[KT * KP];
-    __shared__ __attribute__((aligned(16))) T vts[D * VP];
+    __shared__ __attribute__((aligned(16))) char lds[L::BYTES];
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h2 = lane >> 5, r = lane & 31;
     int64_t bid = blockIdx.x;
     const int64_t nqb = ceil_div(Lq, 32);
     const int64_t qblk = bid % nqb;
     bid /= nqb;
-    const int quad = (int)(bid % quads);
-    bid /= quads;
-    const int64_t hk = bid % HK, b = bid / HK;
-    const int64_t rep = H / HK;
-    const bool active = quad * 4 + wave < rep;
-    const int64_t hq = hk * rep + (active ? quad * 4 + wave : 0);
+    const int64_t hq = bid % H, b = bid / H;
+    const int64_t hk = hq / (H / HK);
     const int64_t q0 = qblk * 32;
     const int64_t off = Lk - Lq;
     const int64_t qrow = q0 + r;
-    const bool qok = active && qrow < Lq;
+    const bool qok = qrow < Lq;
 
     uint4 qf[DS];
     {
@@ -90,52 +105,42 @@ __global__ __launch_bounds__(256) void attn_kernel(const T *__restrict__ q,
     const int ntiles = kend > 0 ? (int)ceil_div(kend, KT) : 0;
     const T *kb = k + (b * HK + hk) * cap * D;
     const T *vb = v + (b * HK + hk) * cap * D;
+    T *vts = (T *)(lds + wave * L::VT_BYTES);  // this wave's V^T tile
 
-    // K/V tile staging: each thread owns CH 16-byte chunks of a tile. The
-    // chunks of tile kt + 1 are loaded into registers while tile kt computes,
-    // so a tile's global-load latency overlaps the previous tile's MFMAs.
-    // Consecutive lanes take consecutive keys: the transposed V stores of a
-    // wave then hit consecutive 2-byte LDS addresses (with the head-dim chunk
-    // fastest, 16 lanes would store into one bank).
-    constexpr int CH = KT * D / 8 / 256;
-    uint4 kreg[CH], vreg[CH];
+    // A tile's loads: the K rows as MFMA A fragments (key r, head-dim chunk
+    // 16 s + 8 h2), and V as 16-byte chunks (key r, chunk h2 + 2 i) for the
+    // transposed LDS tile. Keys past Lk read the last key (in bounds): their
+    // scores are masked and their V rows zeroed.
+    constexpr int VCH = D / 16;  // V chunks per lane
+    uint4 kf[DS], vreg[VCH];
     auto fetch = [&](int kt) {
+        const int64_t kg = (int64_t)kt * KT + r;
+        const int64_t kc = kg < Lk ? kg : Lk - 1;
 #pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            const int c = threadIdx.x + 256 * i;
-            const int key = c % KT, dc = c / KT;
-            const int64_t kg = (int64_t)kt * KT + key;
-            const int64_t kc = kg < Lk ? kg : Lk - 1;  // in bounds; masked below
-            kreg[i] = ld16(kb + kc * D + dc * 8);
-            vreg[i] = ld16(vb + kc * D + dc * 8);
-        }
+        for (int s = 0; s < DS; ++s) kf[s] = ld16(kb + kc * D + 16 * s + 8 * h2);
+#pragma unroll
+        for (int i = 0; i < VCH; ++i) vreg[i] = ld16(vb + kc * D + (h2 + 2 * i) * 8);
     };
-    if (ntiles > 0) fetch(0);
+    if (wave < ntiles) fetch(wave);
 
-    for (int kt = 0; kt < ntiles; ++kt) {
-        __syncthreads();  // every wave is done with tile kt - 1
+    for (int kt = wave; kt < ntiles; kt += ATT_WAVES) {  // wave-uniform
+        // V^T tile: this wave's own LDS, written and read by this wave only
+        // (its LDS instructions execute in order)
+        const bool vok = (int64_t)kt * KT + r < Lk;
 #pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            const int c = threadIdx.x + 256 * i;
-            const int key = c % KT, dc = c / KT;
-            const bool ok = (int64_t)kt * KT + key < Lk;
-            *(uint4 *)(ks + key * KP + dc * 8) = ok ? kreg[i] : make_uint4(0, 0, 0, 0);
-            const V8 vv = __builtin_bit_cast(V8, ok ? vreg[i] : make_uint4(0, 0, 0, 0));
+        for (int i = 0; i < VCH; ++i) {
+            const V8 vv = __builtin_bit_cast(V8, vok ? vreg[i] : make_uint4(0, 0, 0, 0));
+            const int dc = h2 + 2 * i;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) vts[(dc * 8 + e) * VP + key] = vv[e];
+            for (int e = 0; e < 8; ++e) vts[(dc * 8 + e) * VP + r] = vv[e];
         }
-        if (kt + 1 < ntiles) fetch(kt + 1);  // workgroup-uniform
-        __syncthreads();
-        if (!active) continue;
-
         f32x16 s;
 #pragma unroll
         for (int i = 0; i < 16; ++i) s[i] = 0.0f;
 #pragma unroll
-        for (int st = 0; st < DS; ++st) {
-            const V8 a = __builtin_bit_cast(V8, *(const uint4 *)(ks + r * KP + 16 * st + 8 * h2));
-            s = AMfma<T>::mma(a, __builtin_bit_cast(V8, qf[st]), s);
-        }
+        for (int st = 0; st < DS; ++st)
+            s = AMfma<T>::mma(__builtin_bit_cast(V8, kf[st]), __builtin_bit_cast(V8, qf[st]), s);
+        if (kt + ATT_WAVES < ntiles) fetch(kt + ATT_WAVES);  // next tile's loads under this one
         // s[i]: key kt*32 + 8*(i/4) + 4*h2 + i%4 of query row qrow. A tile
         // whose every key every row of the block sees needs no mask.
         float p[16];
@@ -154,7 +159,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const T *__restrict__ q,
         // Lazy rescale: the exponents are taken against a running reference
         // m_run that moves only when a row's maximum passes it by more than
         // 8 (log2 units). p then stays below 2^8, where fp32 sums and the
-        // bf16/fp16 P operand keep their relative precision, and the 64
+        // bf16/fp16 P operand keep their relative precision, and the
         // accumulator rescales run only on those (wave-uniform) steps.
         const bool grow = mt > m_run + 8.0f;
         if (__builtin_amdgcn_ballot_w64(grow) != 0) {
@@ -195,7 +200,37 @@ __global__ __launch_bounds__(256) void attn_kernel(const T *__restrict__ q,
             }
         }
     }
-    if (!qok) return;
+
+    // Merge: waves 1..3 leave (o, l, m) in LDS (over the V^T tiles); wave 0
+    // folds them in, in wave order, each rescaled to the common maximum.
+    float *part = (float *)lds;
+    __syncthreads();  // every wave is done with its V^T tile
+    if (wave > 0) {
+        float *pp = part + (size_t)(wave - 1) * L::PART_FLOATS;
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) pp[(t * 16 + i) * 64 + lane] = o[t][i];
+        pp[DT * 16 * 64 + lane] = l_run;
+        pp[DT * 16 * 64 + 64 + lane] = m_run;
+    }
+    __syncthreads();
+    if (wave > 0 || !qok) return;
+    for (int w = 1; w < ATT_WAVES; ++w) {
+        const float *pp = part + (size_t)(w - 1) * L::PART_FLOATS;
+        const float mw = pp[DT * 16 * 64 + 64 + lane];
+        if (mw == -INFINITY) continue;  // wave w saw no visible key of this row
+        const float lw = pp[DT * 16 * 64 + lane];
+        const float m_new = fmaxf(m_run, mw);
+        const float c0 = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        const float cw = __builtin_amdgcn_exp2f(mw - m_new);
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[t][i] = o[t][i] * c0 + pp[(t * 16 + i) * 64 + lane] * cw;
+        l_run = l_run * c0 + lw * cw;
+        m_run = m_new;
+    }
     const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     T *orow = out_layout ? out + ((b * Lq + qrow) * H + hq) * D
@@ -215,21 +250,17 @@ template <typename T>
 int launch_attn(const void *q, const void *k, const void *v, void *out, int64_t B, int64_t H,
                 int64_t HK, int64_t Lq, int64_t Lk, int64_t D, int64_t cap, float scale,
                 int causal, int out_layout, hipStream_t st) {
-    const int64_t rep = H / HK;
-    const int quads = (int)ceil_div(rep, 4);
-    const int64_t blocks = B * HK * quads * ceil_div(Lq, 32);
+    const int64_t blocks = B * H * ceil_div(Lq, 32);
     if (blocks == 0) return MI_OK;
     const float scale_log2 = scale * 1.4426950408889634f;
     if (D == 128)
-        attn_kernel<T, 128><<<(unsigned)blocks, 256, 0, st>>>((const T *)q, (const T *)k,
-                                                              (const T *)v, (T *)out, H, HK, Lq,
-                                                              Lk, cap, scale_log2, causal,
-                                                              out_layout, quads);
+        attn_kernel<T, 128><<<(unsigned)blocks, 64 * ATT_WAVES, 0, st>>>(
+            (const T *)q, (const T *)k, (const T *)v, (T *)out, H, HK, Lq, Lk, cap, scale_log2,
+            causal, out_layout);
     else
-        attn_kernel<T, 64><<<(unsigned)blocks, 256, 0, st>>>((const T *)q, (const T *)k,
-                                                             (const T *)v, (T *)out, H, HK, Lq,
-                                                             Lk, cap, scale_log2, causal,
-                                                             out_layout, quads);
+        attn_kernel<T, 64><<<(unsigned)blocks, 64 * ATT_WAVES, 0, st>>>(
+            (const T *)q, (const T *)k, (const T *)v, (T *)out, H, HK, Lq, Lk, cap, scale_log2,
+            causal, out_layout);
     return launch_status("sdpa");
 }
 
