@@ -1040,9 +1040,12 @@ int launch_mfma_cfg(QParams p, int wk, hipStream_t st) {
 // 32-feature tile per part (A = P) and 64-token tiles (C = 2) -- the smallest
 // tiles that still reuse each x fragment across two MFMA columns -- give the
 // most workgroups for these narrow-N GEMMs; 32-token tiles when 64-token tiles
-// would leave fewer than 128 workgroups (half the CUs), and 64x128 tiles once
-// the grid exceeds 2048 workgroups (large M), where re-reading x per narrow
-// tile costs more than the lost parallelism.
+// would leave fewer than 128 workgroups (half the CUs). From M = 512 (or past
+// 2048 workgroups) 128-token tiles, two 32-feature tiles per wave for
+// single-part outputs: re-reading x per narrow tile then costs more than the
+// lost parallelism (LFM2 at M = 2048: down_proj 198 -> 99 us, out_proj 42 ->
+// 30 us, the gate/up dual 257 -> 234 us). Tiles never change the numerics:
+// the K split (wk) and each output's accumulation order are fixed by K.
 // K must split into wk slices of whole 64-value x stages. A tile whose rings
 // and scale/bias tables (which grow with K) exceed the LDS steps down to the
 // next smaller one, and past the smallest the GEMV kernel runs instead.
@@ -1052,12 +1055,17 @@ int launch_mfma(const QParams &p, hipStream_t st) {
     const int64_t stages = p.K / XK;
     const int wk = (stages % 4 == 0) ? 4 : (stages % 2 == 0 ? 2 : 1);
     const int64_t nt = ceil_div(p.Nout, 32);
+    const bool large = p.M >= 512 || nt * ceil_div(p.M, 64) > 2048;
     if constexpr (P == 1) {
-        // (8-bit: 32x128, whose stage slots still fit the LDS twice)
-        constexpr int AL = BITS == 4 ? 2 : 1;
-        if (nt * ceil_div(p.M, 64) > 2048 && EPI != EPI_GROUP3 &&
-            mfma_lds_bytes<T, BITS, AL, 4>(p, wk) <= LDS_PER_CU)
+        // (8-bit: 32x128, whose stage slots still fit the LDS twice; the
+        // grouped q/k/v epilogue binds one part per 32-feature tile)
+        constexpr int AL = (BITS == 4 && EPI != EPI_GROUP3) ? 2 : 1;
+        if (large && mfma_lds_bytes<T, BITS, AL, 4>(p, wk) <= LDS_PER_CU)
             return launch_mfma_cfg<T, BITS, AL, 4, EPI>(p, wk, st);
+    }
+    if constexpr (P == 2) {
+        if (large && mfma_lds_bytes<T, BITS, 2, 4>(p, wk) <= LDS_PER_CU)
+            return launch_mfma_cfg<T, BITS, 2, 4, EPI>(p, wk, st);
     }
     if (p.M > 32 && nt * ceil_div(p.M, 64) >= 128 &&
         mfma_lds_bytes<T, BITS, P, 2>(p, wk) <= LDS_PER_CU) {
