@@ -1,29 +1,39 @@
 // Row A7: causal GQA scaled-dot-product attention (mx.fast.scaled_dot_product_attention
 // with mask='causal' or none), flash-style over 32-key tiles.
 //
-// A workgroup is one query head (GQA: kv head of q head h is h / (H/HK),
-// tests/test_graph_model_matrix.py:84-93) on one 32-query block. Its 4 waves
-// split the block's key tiles: wave w takes tiles w, w + 4, w + 8, ... and
-// keeps its own online-softmax state; the 4 partial states are merged at the
-// end in LDS, in wave order. (A prefill of 128 tokens has 4 key tiles for its
-// last block: one per wave, and 32 heads x 4 blocks = 128 workgroups.)
+// The arithmetic of one query row is fixed: its key tiles of 32 (from key 0)
+// are dealt to four streams by tile index (stream w: tiles w, w + 4, ...);
+// each stream runs its own online softmax from scratch; the streams' states
+// are then folded in stream order. Two kernels carry it out, bit for bit
+// alike (same tile-update and merge functions, no floating-point
+// contraction in them):
+//   attn_split_kernel   one workgroup per (q head, 32-row q block); its four
+//                       waves run the four streams side by side and merge in
+//                       LDS. Many workgroups for short sequences (prefill of
+//                       128: 128 workgroups) and for decode.
+//   attn_shared_kernel  one workgroup per (kv head, 4 q heads, 32-row q
+//                       block); its waves are the q heads of one GQA group
+//                       (kv head of q head h is h / (H/HK),
+//                       tests/test_graph_model_matrix.py:84-93) and share
+//                       each K/V tile staged in LDS; each wave runs the
+//                       streams one after another. A quarter of the K/V reads,
+//                       for long sequences.
+// The launcher picks by grid size; the choice never changes a result.
 // Per wave and tile:
-//   S^T[key][q] = K . Q^T   32x32x16 MFMA, A = K rows loaded straight into
-//                           registers (16 bytes per lane and k-step), B = Q^T
-//                           held in registers for the whole kernel;
+//   S^T[key][q] = K . Q^T   32x32x16 MFMA, A = K rows, B = Q^T held in
+//                           registers for the whole kernel;
 //   lane (q = lane%32, half) then holds 16 of the 32 keys of its query row, so
 //   the row max/sum needs one xor-32 shuffle;
-//   O^T[d][q] += V^T . P^T  A = V^T from the wave's own transposed LDS tile,
-//                           B = P^T straight from the S^T registers (bf16/fp16):
-//                           the k order inside each MFMA is permuted to match
-//                           the S^T register layout, for both operands.
+//   O^T[d][q] += V^T . P^T  A = V^T from a transposed LDS tile, B = P^T
+//                           straight from the S^T registers (bf16/fp16): the
+//                           k order inside each MFMA is permuted to match the
+//                           S^T register layout, for both operands.
 // Online softmax in the log2 domain, fp32 running max/sum, one division at
 // the end. Causal masking is bottom-right aligned (query i sees keys
 // j <= i + Lk - Lq) and key tiles past the last visible key are skipped.
-// A query row's result depends only on its global position and the keys'
-// (tiles of 32 from key 0, dealt to waves by tile index), so a chunked
-// prefill whose chunks start at multiples of 32 reproduces the whole prefill
-// bit for bit.
+// A row's result depends only on its global position and the keys, so a
+// chunked prefill whose chunks start at multiples of 32 reproduces the whole
+// prefill bit for bit.
 #include <math.h>
 
 #include "mi_common.h"
@@ -43,31 +53,162 @@ template <> struct AMfma<f16> {
     }
 };
 
-constexpr int ATT_WAVES = 4;  // key-tile splits per workgroup
+constexpr int ATT_KT = 32;       // keys per tile
+constexpr int ATT_VP = ATT_KT + 8;  // padded V^T-tile row (elements)
+constexpr int ATT_STREAMS = 4;   // key-tile streams per query row
 
-// LDS of one workgroup: the waves' V^T tiles, reused afterwards for the
-// partial states of waves 1..3 (o: DT x 16 floats per lane; l, m per lane).
-template <int D> struct AttnLds {
-    static constexpr int KT = 32;
-    static constexpr int VP = KT + 8;  // padded V^T-tile row (elements)
+// Online-softmax state of one wave: O^T tiles (lane = query column r, half
+// h2), the row's reference maximum m (log2 units) and this lane's half of the
+// row sum l.
+template <int D> struct AttnState {
+    f32x16 o[D / 32];
+    float m, l;
+};
+
+template <int D> __device__ __forceinline__ void attn_init(AttnState<D> &st) {
+#pragma unroll
+    for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) st.o[t][i] = 0.0f;
+    st.m = -INFINITY;
+    st.l = 0.0f;
+}
+
+// One key tile kt: s = S^T (s[i]: key kt*32 + 8*(i/4) + 4*h2 + i%4 of query
+// row qrow), vts = the tile's V^T in LDS (D rows of ATT_VP). Masking, the
+// lazily rescaled online softmax, O^T += V^T . P^T.
+template <typename T, int D>
+__device__ __forceinline__ void attn_tile(AttnState<D> &st, const f32x16 &s, const T *vts, int kt,
+                                          int64_t q0, int64_t qrow, int64_t off, int64_t Lk,
+                                          int causal, float scale_log2, int h2, int r) {
+#pragma clang fp contract(off)
+    constexpr int DT = D / 32;
+    typedef typename Vec<T>::x8 V8;
+    typedef typename Vec<T>::x4 V4;
+    float p[16];
+    float mt = -INFINITY;
+    // a tile whose every key every row of the block sees needs no mask
+    const bool full = (int64_t)kt * ATT_KT + ATT_KT <= Lk &&
+                      (!causal || (int64_t)kt * ATT_KT + ATT_KT - 1 <= q0 + off);
+    const int vis_end = (int)((causal && qrow + off + 1 < Lk ? qrow + off + 1 : Lk) -
+                              (int64_t)kt * ATT_KT);  // keys [0, vis_end) of the tile
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int kl = 8 * (i / 4) + 4 * h2 + (i % 4);
+        p[i] = (full || kl < vis_end) ? s[i] * scale_log2 : -INFINITY;
+        mt = fmaxf(mt, p[i]);
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    // Lazy rescale: the exponents are taken against a running reference m
+    // that moves only when a row's maximum passes it by more than 8 (log2
+    // units). p then stays below 2^8, where fp32 sums and the bf16/fp16 P
+    // operand keep their relative precision, and the accumulator rescales run
+    // only on those (wave-uniform) steps.
+    const bool grow = mt > st.m + 8.0f;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        const float m_new = grow ? mt : st.m;
+        const float corr = st.m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(st.m - m_new);
+        st.l *= corr;
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) st.o[t][i] *= corr;
+        st.m = m_new;
+    }
+    const bool none = st.m == -INFINITY;
+    float psum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        p[i] = none ? 0.0f : __builtin_amdgcn_exp2f(p[i] - st.m);
+        psum += p[i];
+    }
+    st.l += psum;
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+        V8 pb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pb[e] = (T)p[8 * k2 + e];
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            const T *vr = vts + (32 * t + r) * ATT_VP + 16 * k2 + 4 * h2;
+            const V4 lo = __builtin_bit_cast(V4, *(const uint2 *)vr);
+            const V4 hi = __builtin_bit_cast(V4, *(const uint2 *)(vr + 8));
+            V8 a;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                a[e] = lo[e];
+                a[4 + e] = hi[e];
+            }
+            st.o[t] = AMfma<T>::mma(a, pb, st.o[t]);
+        }
+    }
+}
+
+// Fold a later stream's state (mw, lw, ow(t, i)) into st. A stream that saw
+// no visible key of the row (mw = -inf) leaves st as it is.
+template <int D, typename OW>
+__device__ __forceinline__ void attn_merge(AttnState<D> &st, float mw, float lw, OW ow) {
+#pragma clang fp contract(off)
+    if (mw == -INFINITY) return;
+    const float m_new = fmaxf(st.m, mw);
+    const float c0 = st.m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(st.m - m_new);
+    const float cw = __builtin_amdgcn_exp2f(mw - m_new);
+#pragma unroll
+    for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) st.o[t][i] = __builtin_fmaf(st.o[t][i], c0, ow(t, i) * cw);
+    st.l = __builtin_fmaf(st.l, c0, lw * cw);
+    st.m = m_new;
+}
+
+// O = O^T / row sum, stored as the lane's query row.
+template <typename T, int D>
+__device__ __forceinline__ void attn_store(const AttnState<D> &st, T *orow, int h2) {
+#pragma clang fp contract(off)
+    const float l_tot = st.l + __shfl_xor(st.l, 32, 64);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+#pragma unroll
+    for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) {
+            float f[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) f[e] = st.o[t][4 * blk + e] * inv;
+            st8(orow + 32 * t + 8 * blk + 4 * h2, pack4<T>(f));
+        }
+}
+
+// Key tiles visible to a q block (causal: up to its last row).
+__device__ __forceinline__ int attn_ntiles(int64_t q0, int64_t off, int64_t Lk, int causal) {
+    int64_t kend = Lk;
+    if (causal) {
+        const int64_t last = q0 + 31 + off + 1;
+        kend = last < Lk ? last : Lk;
+    }
+    return kend > 0 ? (int)ceil_div(kend, ATT_KT) : 0;
+}
+
+// ---------------------------------------------------------------------------
+// attn_split_kernel: workgroup = (q head, q block); wave w runs stream w.
+
+template <int D> struct SplitLds {
     static constexpr int DT = D / 32;
-    static constexpr int VT_BYTES = D * VP * 2;                           // one wave's V^T tile
-    static constexpr int PART_FLOATS = DT * 16 * 64 + 2 * 64;             // one wave's state
-    static constexpr int BYTES = ATT_WAVES * VT_BYTES > (ATT_WAVES - 1) * PART_FLOATS * 4
-                                     ? ATT_WAVES * VT_BYTES
-                                     : (ATT_WAVES - 1) * PART_FLOATS * 4;
+    static constexpr int VT_BYTES = D * ATT_VP * 2;            // one wave's V^T tile
+    static constexpr int PART_FLOATS = DT * 16 * 64 + 2 * 64;  // one wave's state
+    static constexpr int BYTES = ATT_STREAMS * VT_BYTES > (ATT_STREAMS - 1) * PART_FLOATS * 4
+                                     ? ATT_STREAMS * VT_BYTES
+                                     : (ATT_STREAMS - 1) * PART_FLOATS * 4;
 };
 
 template <typename T, int D>
-__global__ __launch_bounds__(64 * ATT_WAVES) void attn_kernel(
+__global__ __launch_bounds__(64 * ATT_STREAMS) void attn_split_kernel(
     const T *__restrict__ q, const T *__restrict__ k, const T *__restrict__ v,
     T *__restrict__ out, int64_t H, int64_t HK, int64_t Lq, int64_t Lk, int64_t cap,
     float scale_log2, int causal, int out_layout) {
-    typedef AttnLds<D> L;
-    constexpr int KT = L::KT, VP = L::VP, DT = L::DT;
+    typedef SplitLds<D> L;
+    constexpr int DT = D / 32;
     constexpr int DS = D / 16;  // MFMA k-steps over the head dim
     typedef typename Vec<T>::x8 V8;
-    typedef typename Vec<T>::x4 V4;
     __shared__ __attribute__((aligned(16))) char lds[L::BYTES];
 
     const int lane = threadIdx.x & 63;
@@ -90,19 +231,9 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_kernel(
 #pragma unroll
         for (int s = 0; s < DS; ++s) qf[s] = qok ? ld16(qp + 16 * s) : make_uint4(0, 0, 0, 0);
     }
-    f32x16 o[DT];
-#pragma unroll
-    for (int t = 0; t < DT; ++t)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[t][i] = 0.0f;
-    float m_run = -INFINITY, l_run = 0.0f;
-
-    int64_t kend = Lk;
-    if (causal) {
-        const int64_t last = q0 + 31 + off + 1;  // keys visible to the block's last row
-        kend = last < Lk ? last : Lk;
-    }
-    const int ntiles = kend > 0 ? (int)ceil_div(kend, KT) : 0;
+    AttnState<D> st;
+    attn_init(st);
+    const int ntiles = attn_ntiles(q0, off, Lk, causal);
     const T *kb = k + (b * HK + hk) * cap * D;
     const T *vb = v + (b * HK + hk) * cap * D;
     T *vts = (T *)(lds + wave * L::VT_BYTES);  // this wave's V^T tile
@@ -114,7 +245,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_kernel(
     constexpr int VCH = D / 16;  // V chunks per lane
     uint4 kf[DS], vreg[VCH];
     auto fetch = [&](int kt) {
-        const int64_t kg = (int64_t)kt * KT + r;
+        const int64_t kg = (int64_t)kt * ATT_KT + r;
         const int64_t kc = kg < Lk ? kg : Lk - 1;
 #pragma unroll
         for (int s = 0; s < DS; ++s) kf[s] = ld16(kb + kc * D + 16 * s + 8 * h2);
@@ -123,86 +254,29 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_kernel(
     };
     if (wave < ntiles) fetch(wave);
 
-    for (int kt = wave; kt < ntiles; kt += ATT_WAVES) {  // wave-uniform
+    for (int kt = wave; kt < ntiles; kt += ATT_STREAMS) {  // wave-uniform
         // V^T tile: this wave's own LDS, written and read by this wave only
         // (its LDS instructions execute in order)
-        const bool vok = (int64_t)kt * KT + r < Lk;
+        const bool vok = (int64_t)kt * ATT_KT + r < Lk;
 #pragma unroll
         for (int i = 0; i < VCH; ++i) {
             const V8 vv = __builtin_bit_cast(V8, vok ? vreg[i] : make_uint4(0, 0, 0, 0));
             const int dc = h2 + 2 * i;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) vts[(dc * 8 + e) * VP + r] = vv[e];
+            for (int e = 0; e < 8; ++e) vts[(dc * 8 + e) * ATT_VP + r] = vv[e];
         }
         f32x16 s;
 #pragma unroll
         for (int i = 0; i < 16; ++i) s[i] = 0.0f;
 #pragma unroll
-        for (int st = 0; st < DS; ++st)
-            s = AMfma<T>::mma(__builtin_bit_cast(V8, kf[st]), __builtin_bit_cast(V8, qf[st]), s);
-        if (kt + ATT_WAVES < ntiles) fetch(kt + ATT_WAVES);  // next tile's loads under this one
-        // s[i]: key kt*32 + 8*(i/4) + 4*h2 + i%4 of query row qrow. A tile
-        // whose every key every row of the block sees needs no mask.
-        float p[16];
-        float mt = -INFINITY;
-        const bool full = (int64_t)kt * KT + KT <= Lk &&
-                          (!causal || (int64_t)kt * KT + KT - 1 <= q0 + off);
-        const int vis_end = (int)((causal && qrow + off + 1 < Lk ? qrow + off + 1 : Lk) -
-                                  (int64_t)kt * KT);  // keys [0, vis_end) of the tile
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int kl = 8 * (i / 4) + 4 * h2 + (i % 4);
-            p[i] = (full || kl < vis_end) ? s[i] * scale_log2 : -INFINITY;
-            mt = fmaxf(mt, p[i]);
-        }
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-        // Lazy rescale: the exponents are taken against a running reference
-        // m_run that moves only when a row's maximum passes it by more than
-        // 8 (log2 units). p then stays below 2^8, where fp32 sums and the
-        // bf16/fp16 P operand keep their relative precision, and the
-        // accumulator rescales run only on those (wave-uniform) steps.
-        const bool grow = mt > m_run + 8.0f;
-        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-            const float m_new = grow ? mt : m_run;
-            const float corr = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-            l_run *= corr;
-#pragma unroll
-            for (int t = 0; t < DT; ++t)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) o[t][i] *= corr;
-            m_run = m_new;
-        }
-        const bool none = m_run == -INFINITY;
-        float psum = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            p[i] = none ? 0.0f : __builtin_amdgcn_exp2f(p[i] - m_run);
-            psum += p[i];
-        }
-        l_run += psum;
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            V8 pb;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) pb[e] = (T)p[8 * st + e];
-#pragma unroll
-            for (int t = 0; t < DT; ++t) {
-                const T *vr = vts + (32 * t + r) * VP + 16 * st + 4 * h2;
-                const V4 lo = __builtin_bit_cast(V4, *(const uint2 *)vr);
-                const V4 hi = __builtin_bit_cast(V4, *(const uint2 *)(vr + 8));
-                V8 a;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    a[e] = lo[e];
-                    a[4 + e] = hi[e];
-                }
-                o[t] = AMfma<T>::mma(a, pb, o[t]);
-            }
-        }
+        for (int ks = 0; ks < DS; ++ks)
+            s = AMfma<T>::mma(__builtin_bit_cast(V8, kf[ks]), __builtin_bit_cast(V8, qf[ks]), s);
+        if (kt + ATT_STREAMS < ntiles) fetch(kt + ATT_STREAMS);  // under this tile's math
+        attn_tile<T, D>(st, s, vts, kt, q0, qrow, off, Lk, causal, scale_log2, h2, r);
     }
 
     // Merge: waves 1..3 leave (o, l, m) in LDS (over the V^T tiles); wave 0
-    // folds them in, in wave order, each rescaled to the common maximum.
+    // folds them in, in stream order.
     float *part = (float *)lds;
     __syncthreads();  // every wave is done with its V^T tile
     if (wave > 0) {
@@ -210,58 +284,165 @@ __global__ __launch_bounds__(64 * ATT_WAVES) void attn_kernel(
 #pragma unroll
         for (int t = 0; t < DT; ++t)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) pp[(t * 16 + i) * 64 + lane] = o[t][i];
-        pp[DT * 16 * 64 + lane] = l_run;
-        pp[DT * 16 * 64 + 64 + lane] = m_run;
+            for (int i = 0; i < 16; ++i) pp[(t * 16 + i) * 64 + lane] = st.o[t][i];
+        pp[DT * 16 * 64 + lane] = st.l;
+        pp[DT * 16 * 64 + 64 + lane] = st.m;
     }
     __syncthreads();
     if (wave > 0 || !qok) return;
-    for (int w = 1; w < ATT_WAVES; ++w) {
+    for (int w = 1; w < ATT_STREAMS; ++w) {
         const float *pp = part + (size_t)(w - 1) * L::PART_FLOATS;
-        const float mw = pp[DT * 16 * 64 + 64 + lane];
-        if (mw == -INFINITY) continue;  // wave w saw no visible key of this row
-        const float lw = pp[DT * 16 * 64 + lane];
-        const float m_new = fmaxf(m_run, mw);
-        const float c0 = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-        const float cw = __builtin_amdgcn_exp2f(mw - m_new);
-#pragma unroll
-        for (int t = 0; t < DT; ++t)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) o[t][i] = o[t][i] * c0 + pp[(t * 16 + i) * 64 + lane] * cw;
-        l_run = l_run * c0 + lw * cw;
-        m_run = m_new;
+        attn_merge(st, pp[DT * 16 * 64 + 64 + lane], pp[DT * 16 * 64 + lane],
+                   [&](int t, int i) { return pp[(t * 16 + i) * 64 + lane]; });
     }
-    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     T *orow = out_layout ? out + ((b * Lq + qrow) * H + hq) * D
                          : out + ((b * H + hq) * Lq + qrow) * D;
+    attn_store<T, D>(st, orow, h2);
+}
+
+// ---------------------------------------------------------------------------
+// attn_shared_kernel: workgroup = (kv head, quad of its q heads, q block);
+// the four waves share each K/V tile and run the streams in turn.
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_shared_kernel(
+    const T *__restrict__ q, const T *__restrict__ k, const T *__restrict__ v,
+    T *__restrict__ out, int64_t H, int64_t HK, int64_t Lq, int64_t Lk, int64_t cap,
+    float scale_log2, int causal, int out_layout, int quads) {
+    constexpr int KP = D + 8;  // padded K-tile row (elements)
+    constexpr int DS = D / 16;
+    typedef typename Vec<T>::x8 V8;
+    __shared__ __attribute__((aligned(16))) T ks[ATT_KT * KP];
+    __shared__ __attribute__((aligned(16))) T vts[D * ATT_VP];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int h2 = lane >> 5, r = lane & 31;
+    int64_t bid = blockIdx.x;
+    const int64_t nqb = ceil_div(Lq, 32);
+    const int64_t qblk = bid % nqb;
+    bid /= nqb;
+    const int quad = (int)(bid % quads);
+    bid /= quads;
+    const int64_t hk = bid % HK, b = bid / HK;
+    const int64_t rep = H / HK;
+    const bool active = quad * 4 + wave < rep;
+    const int64_t hq = hk * rep + (active ? quad * 4 + wave : 0);
+    const int64_t q0 = qblk * 32;
+    const int64_t off = Lk - Lq;
+    const int64_t qrow = q0 + r;
+    const bool qok = active && qrow < Lq;
+
+    uint4 qf[DS];
+    {
+        const T *qp = q + ((b * H + hq) * Lq + (qok ? qrow : 0)) * D + 8 * h2;
 #pragma unroll
-    for (int t = 0; t < DT; ++t)
+        for (int s = 0; s < DS; ++s) qf[s] = qok ? ld16(qp + 16 * s) : make_uint4(0, 0, 0, 0);
+    }
+    const int ntiles = attn_ntiles(q0, off, Lk, causal);
+    const T *kb = k + (b * HK + hk) * cap * D;
+    const T *vb = v + (b * HK + hk) * cap * D;
+
+    // K/V tile staging: each thread owns CH 16-byte chunks of a tile; the
+    // chunks of the next tile are loaded into registers while this one
+    // computes. Consecutive lanes take consecutive keys, so the transposed V
+    // stores of a wave hit consecutive 2-byte LDS addresses.
+    constexpr int CH = ATT_KT * D / 8 / 256;
+    uint4 kreg[CH], vreg[CH];
+    auto fetch = [&](int kt) {
 #pragma unroll
-        for (int blk = 0; blk < 4; ++blk) {
-            float f[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) f[e] = o[t][4 * blk + e] * inv;
-            st8(orow + 32 * t + 8 * blk + 4 * h2, pack4<T>(f));
+        for (int i = 0; i < CH; ++i) {
+            const int c = threadIdx.x + 256 * i;
+            const int key = c % ATT_KT, dc = c / ATT_KT;
+            const int64_t kg = (int64_t)kt * ATT_KT + key;
+            const int64_t kc = kg < Lk ? kg : Lk - 1;  // in bounds; masked below
+            kreg[i] = ld16(kb + kc * D + dc * 8);
+            vreg[i] = ld16(vb + kc * D + dc * 8);
         }
+    };
+    // tiles in stream order: 0, 4, 8, ..., then 1, 5, 9, ..., and so on
+    auto next_tile = [&](int kt) -> int {
+        if (kt + ATT_STREAMS < ntiles) return kt + ATT_STREAMS;
+        const int s = kt % ATT_STREAMS + 1;
+        return s < ATT_STREAMS && s < ntiles ? s : -1;
+    };
+    AttnState<D> tot, cur;
+    attn_init(tot);
+    attn_init(cur);
+    if (ntiles > 0) fetch(0);
+    for (int kt = ntiles > 0 ? 0 : -1; kt >= 0;) {  // workgroup-uniform
+        __syncthreads();  // every wave is done with the previous tile
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int c = threadIdx.x + 256 * i;
+            const int key = c % ATT_KT, dc = c / ATT_KT;
+            const bool ok = (int64_t)kt * ATT_KT + key < Lk;
+            *(uint4 *)(ks + key * KP + dc * 8) = ok ? kreg[i] : make_uint4(0, 0, 0, 0);
+            const V8 vv = __builtin_bit_cast(V8, ok ? vreg[i] : make_uint4(0, 0, 0, 0));
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vts[(dc * 8 + e) * ATT_VP + key] = vv[e];
+        }
+        const int nk = next_tile(kt);
+        if (nk >= 0) fetch(nk);
+        __syncthreads();
+        if (active) {
+            f32x16 s;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+#pragma unroll
+            for (int kq = 0; kq < DS; ++kq) {
+                const V8 a =
+                    __builtin_bit_cast(V8, *(const uint4 *)(ks + r * KP + 16 * kq + 8 * h2));
+                s = AMfma<T>::mma(a, __builtin_bit_cast(V8, qf[kq]), s);
+            }
+            attn_tile<T, D>(cur, s, vts, kt, q0, qrow, off, Lk, causal, scale_log2, h2, r);
+            if (nk < 0 || nk % ATT_STREAMS != kt % ATT_STREAMS) {  // stream kt % 4 ends
+                if (kt % ATT_STREAMS == 0)
+                    tot = cur;
+                else
+                    attn_merge(tot, cur.m, cur.l, [&](int t, int i) { return cur.o[t][i]; });
+                attn_init(cur);
+            }
+        }
+        kt = nk;
+    }
+    if (!qok) return;
+    T *orow = out_layout ? out + ((b * Lq + qrow) * H + hq) * D
+                         : out + ((b * H + hq) * Lq + qrow) * D;
+    attn_store<T, D>(tot, orow, h2);
+}
+
+// The shared-K/V kernel once its grid fills half the CUs (256 CUs on MI355X);
+// the split kernel below that (short prefill, decode). Same results either way.
+constexpr int64_t ATT_SHARED_MIN_BLOCKS = 128;
+
+template <typename T, int D>
+int launch_attn_d(const void *q, const void *k, const void *v, void *out, int64_t B, int64_t H,
+                  int64_t HK, int64_t Lq, int64_t Lk, int64_t cap, float scale_log2, int causal,
+                  int out_layout, hipStream_t st) {
+    const int quads = (int)ceil_div(H / HK, 4);
+    const int64_t shared_blocks = B * HK * quads * ceil_div(Lq, 32);
+    if (shared_blocks >= ATT_SHARED_MIN_BLOCKS)
+        attn_shared_kernel<T, D><<<(unsigned)shared_blocks, 256, 0, st>>>(
+            (const T *)q, (const T *)k, (const T *)v, (T *)out, H, HK, Lq, Lk, cap, scale_log2,
+            causal, out_layout, quads);
+    else
+        attn_split_kernel<T, D><<<(unsigned)(B * H * ceil_div(Lq, 32)), 64 * ATT_STREAMS, 0, st>>>(
+            (const T *)q, (const T *)k, (const T *)v, (T *)out, H, HK, Lq, Lk, cap, scale_log2,
+            causal, out_layout);
+    return launch_status("sdpa");
 }
 
 template <typename T>
 int launch_attn(const void *q, const void *k, const void *v, void *out, int64_t B, int64_t H,
                 int64_t HK, int64_t Lq, int64_t Lk, int64_t D, int64_t cap, float scale,
                 int causal, int out_layout, hipStream_t st) {
-    const int64_t blocks = B * H * ceil_div(Lq, 32);
-    if (blocks == 0) return MI_OK;
+    if (B * H * ceil_div(Lq, 32) == 0) return MI_OK;
     const float scale_log2 = scale * 1.4426950408889634f;
     if (D == 128)
-        attn_kernel<T, 128><<<(unsigned)blocks, 64 * ATT_WAVES, 0, st>>>(
-            (const T *)q, (const T *)k, (const T *)v, (T *)out, H, HK, Lq, Lk, cap, scale_log2,
-            causal, out_layout);
-    else
-        attn_kernel<T, 64><<<(unsigned)blocks, 64 * ATT_WAVES, 0, st>>>(
-            (const T *)q, (const T *)k, (const T *)v, (T *)out, H, HK, Lq, Lk, cap, scale_log2,
-            causal, out_layout);
-    return launch_status("sdpa");
+        return launch_attn_d<T, 128>(q, k, v, out, B, H, HK, Lq, Lk, cap, scale_log2, causal,
+                                     out_layout, st);
+    return launch_attn_d<T, 64>(q, k, v, out, B, H, HK, Lq, Lk, cap, scale_log2, causal,
+                                out_layout, st);
 }
 
 }  // namespace

@@ -317,7 +317,9 @@ def test_norm_rope_qkv_equals_three_calls(L, offset, strided):
                                                  (32, 8, 200, 200, 64, True),
                                                  (8, 8, 40, 70, 64, True),
                                                  (6, 2, 33, 33, 128, False),
-                                                 (12, 4, 5, 130, 128, True)])
+                                                 (12, 4, 5, 130, 128, True),
+                                                 (32, 8, 512, 512, 64, True),      # shared-K/V kernel
+                                                 (16, 2, 1000, 1030, 128, True)])  # shared, 2 quads
 def test_sdpa(H, HK, Lq, Lk, D, causal):
     r = rng(1000 + Lq + Lk + D)
     q = oracle.round_to(r.normal(0, 1, (1, H, Lq, D)), "bfloat16")
@@ -332,6 +334,25 @@ def test_sdpa(H, HK, Lq, Lk, D, causal):
                                           to_torch(v, "bfloat16"), scale,
                                           "causal" if causal else None, out_layout=1)
     assert torch.equal(o1, o.transpose(1, 2).contiguous())
+
+
+@pytest.mark.parametrize("H,HK,L,D,causal", [(32, 8, 512, 64, True), (16, 2, 1024, 128, True),
+                                             (32, 8, 512, 128, False)])
+def test_sdpa_shared_and_split_kernels_agree(H, HK, L, D, causal):
+    """A row's attention is the same bits whichever kernel computes it. The
+    L-row call runs the shared-K/V kernel (a grid of at least 128
+    workgroups); a call on its last 32 query rows, and a decode call on its
+    last row, run the key-split kernel (smaller grids) over the same keys."""
+    r = rng(1050 + L + D)
+    q = to_torch(oracle.round_to(r.normal(0, 1, (1, H, L, D)), "bfloat16"), "bfloat16")
+    k = to_torch(oracle.round_to(r.normal(0, 1, (1, HK, L, D)), "bfloat16"), "bfloat16")
+    v = to_torch(oracle.round_to(r.normal(0, 1, (1, HK, L, D)), "bfloat16"), "bfloat16")
+    mask = "causal" if causal else None
+    full = ops.scaled_dot_product_attention(q, k, v, D ** -0.5, mask)
+    tail = ops.scaled_dot_product_attention(q[:, :, L - 32:].contiguous(), k, v, D ** -0.5, mask)
+    last = ops.scaled_dot_product_attention(q[:, :, L - 1:].contiguous(), k, v, D ** -0.5, mask)
+    assert torch.equal(full[:, :, L - 32:], tail)
+    assert torch.equal(full[:, :, L - 1:], last)
 
 
 def test_sdpa_kv_cache_capacity():
