@@ -38,7 +38,11 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const T *__restrict__ g,
 
 // Grid rows 0..L-1 produce out; rows L, L+1 copy the last two padded rows into
 // state_out. pad[i] = state_in[i] (or 0) for i < 2, bx[i-2] otherwise.
-template <typename T>
+// VEC (D a multiple of 8, every pointer 16-byte aligned): a thread's 8
+// channels move as 16-byte loads and stores -- the three taps of bx, c, the
+// 24 weights (w is [D, 3], so 8 channels' weights are 48 contiguous bytes),
+// the state rows -- with the same per-channel arithmetic as the scalar path.
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void shortconv_kernel(const T *__restrict__ bx,
                                                         const T *__restrict__ c,
                                                         const T *__restrict__ w,
@@ -50,6 +54,49 @@ __global__ __launch_bounds__(256) void shortconv_kernel(const T *__restrict__ bx
     const int64_t dchunks = ceil_div(D, 8);
     if (t >= B * (L + 2) * dchunks) return;
     const int64_t dc = t % dchunks, row = (t / dchunks) % (L + 2), b = t / (dchunks * (L + 2));
+    if constexpr (VEC && sizeof(T) == 2) {
+        const int64_t d0 = dc * 8;
+        auto padv = [&](int64_t i, float (&f)[8]) {
+            if (i >= 2) {
+                unpack8<T>(ld16(bx + (b * L + i - 2) * D + d0), f);
+            } else if (st_in) {
+                unpack8<T>(ld16(st_in + (b * 2 + i) * D + d0), f);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) f[e] = 0.0f;
+            }
+        };
+        if (row < L) {
+            float p0[8], p1[8], p2[8], cf[8], wf[24];
+            padv(row, p0);
+            padv(row + 1, p1);
+            padv(row + 2, p2);
+            unpack8<T>(ld16(c + (b * L + row) * D + d0), cf);
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                float tmp[8];
+                unpack8<T>(ld16(w + d0 * 3 + 8 * j), tmp);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) wf[8 * j + e] = tmp[e];
+            }
+            float o[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float acc = p0[e] * wf[3 * e + 0];
+                acc = __builtin_fmaf(p1[e], wf[3 * e + 1], acc);
+                acc = __builtin_fmaf(p2[e], wf[3 * e + 2], acc);
+                const float conv = (float)cvt<T>(acc);
+                o[e] = cf[e] * conv;
+            }
+            st16(out + (b * L + row) * D + d0, pack8<T>(o));
+        } else if (st_out) {
+            const int64_t i = row - L;  // 0 or 1
+            float f[8];
+            padv(L + i, f);
+            st16(st_out + (b * 2 + i) * D + d0, pack8<T>(f));
+        }
+        return;
+    }
     auto pad = [&](int64_t i, int64_t d) -> float {
         if (i >= 2) return (float)bx[(b * L + i - 2) * D + d];
         return st_in ? (float)st_in[(b * 2 + i) * D + d] : 0.0f;
@@ -308,10 +355,20 @@ extern "C" int mi_shortconv(const void *bx, const void *c, const void *w, const 
     if (threads == 0) return MI_OK;
     hipStream_t st = as_stream(stream);
     const unsigned grid = (unsigned)ceil_div(threads, 256);
+    const bool vec = D % 8 == 0 && aligned(bx, 16) && aligned(c, 16) && aligned(w, 16) &&
+                     aligned(out, 16) && (!state_in || aligned(state_in, 16)) &&
+                     (!state_out || aligned(state_out, 16));
 #define MI_SC(TT)                                                                               \
-    shortconv_kernel<TT><<<grid, 256, 0, st>>>((const TT *)bx, (const TT *)c, (const TT *)w,    \
-                                               (const TT *)state_in, (TT *)out, (TT *)state_out, \
-                                               B, L, D)
+    do {                                                                                        \
+        if (vec)                                                                                \
+            shortconv_kernel<TT, true><<<grid, 256, 0, st>>>(                                   \
+                (const TT *)bx, (const TT *)c, (const TT *)w, (const TT *)state_in, (TT *)out,  \
+                (TT *)state_out, B, L, D);                                                      \
+        else                                                                                    \
+            shortconv_kernel<TT, false><<<grid, 256, 0, st>>>(                                  \
+                (const TT *)bx, (const TT *)c, (const TT *)w, (const TT *)state_in, (TT *)out,  \
+                (TT *)state_out, B, L, D);                                                      \
+    } while (0)
     if (dtype == MI_BF16)
         MI_SC(bf16);
     else if (dtype == MI_F16)

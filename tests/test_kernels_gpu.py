@@ -391,6 +391,12 @@ def test_shortconv(L, with_state):
     want, st_want = oracle.shortconv(bx, c, w, st, "bfloat16")
     _close(out, want, "bfloat16")
     assert np.array_equal(to_np(st_out), st_want)
+    # the scalar path (bx one element off 16-byte alignment) gives the same bits
+    flat = to_torch(np.concatenate([[0.0], bx.reshape(-1)]).astype(np.float32), "bfloat16")
+    bx_odd = flat[1:].reshape(B, L, D)
+    out2, st_out2 = ops.shortconv(bx_odd, to_torch(c, "bfloat16"), to_torch(w, "bfloat16"),
+                                  None if st is None else to_torch(st, "bfloat16"))
+    assert torch.equal(out, out2) and torch.equal(st_out, st_out2)
 
 
 def test_linear_gelu_f32():
