@@ -69,38 +69,54 @@ template <typename T> __device__ __forceinline__ uint2 pack4(const float (&f)[4]
     return __builtin_bit_cast(uint2, v);
 }
 
-// Affine dequant of the 8 consecutive values starting at nibble/byte `first`
-// of a packed chunk: T(fma(s, q, b)), one rounding (the reference's dequant
-// form). For 4 bits the 8 values are the 8 nibbles of word w0; for 8 bits
-// they are the 4 bytes of w0 followed by the 4 bytes of w1.
-template <typename T, int BITS>
-__device__ __forceinline__ typename Vec<T>::x8 dequant8(uint32_t w0, uint32_t w1, float s,
-                                                       float b) {
+// Affine dequant of 8 consecutive packed values: T(fma(s, q, b)), one
+// rounding (the reference's dequant form). For 4 bits the 8 values are the 8
+// nibbles of word w0; for 8 bits they are the 4 bytes of w0 followed by the 4
+// bytes of w1. init() prepares the words once; pair(k) converts values 2k and
+// 2k + 1 into one packed register, so a caller can spread the four pairs
+// between other instructions.
+template <typename T, int BITS> struct Dequant8 {
+    uint32_t a, b;  // 4 bits: even / odd nibbles as bytes; 8 bits: w0, w1
+    float s, bias;
+
+    __device__ __forceinline__ void init(uint32_t w0, uint32_t w1, float s_, float b_) {
+        s = s_;
+        bias = b_;
+        if constexpr (BITS == 4) {
+            // even nibbles to the bytes of a, odd nibbles to the bytes of b,
+            // so each value converts with one v_cvt_f32_ubyte{0..3}; the empty
+            // asm hides the masks, which would otherwise be folded back into
+            // one shift-and-mask per nibble
+            a = w0 & 0x0F0F0F0Fu;
+            b = (w0 >> 4) & 0x0F0F0F0Fu;
+            asm("" : "+v"(a), "+v"(b));
+        } else {
+            a = w0;
+            b = w1;
+        }
+    }
     // Values 2k and 2k + 1 are converted together (pk2): converted one by
     // one, the compiler packed mismatched pairs and re-shuffled them, five
     // extra VALU per 8 values.
-    uint32_t r[4];
-    if constexpr (BITS == 4) {
-        // even nibbles to the bytes of lo, odd nibbles to the bytes of hi, so
-        // each value converts with one v_cvt_f32_ubyte{0..3}; the empty asm
-        // hides the masks, which would otherwise be folded back into one
-        // shift-and-mask per nibble
-        uint32_t lo = w0 & 0x0F0F0F0Fu, hi = (w0 >> 4) & 0x0F0F0F0Fu;
-        asm("" : "+v"(lo), "+v"(hi));
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            r[k] = pk2<T>(__builtin_fmaf(s, (float)((lo >> (8 * k)) & 255u), b),
-                          __builtin_fmaf(s, (float)((hi >> (8 * k)) & 255u), b));
-    } else {
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            r[k] = pk2<T>(__builtin_fmaf(s, (float)((w0 >> (16 * k)) & 255u), b),
-                          __builtin_fmaf(s, (float)((w0 >> (16 * k + 8)) & 255u), b));
-            r[2 + k] = pk2<T>(__builtin_fmaf(s, (float)((w1 >> (16 * k)) & 255u), b),
-                              __builtin_fmaf(s, (float)((w1 >> (16 * k + 8)) & 255u), b));
+    __device__ __forceinline__ uint32_t pair(int k) const {
+        if constexpr (BITS == 4) {
+            return pk2<T>(__builtin_fmaf(s, (float)((a >> (8 * k)) & 255u), bias),
+                          __builtin_fmaf(s, (float)((b >> (8 * k)) & 255u), bias));
+        } else {
+            const uint32_t w = k < 2 ? a : b;
+            const int sh = 16 * (k & 1);
+            return pk2<T>(__builtin_fmaf(s, (float)((w >> sh) & 255u), bias),
+                          __builtin_fmaf(s, (float)((w >> (sh + 8)) & 255u), bias));
         }
     }
-    return __builtin_bit_cast(typename Vec<T>::x8, (uint4){r[0], r[1], r[2], r[3]});
+};
+
+template <typename T, int BITS>
+__device__ __forceinline__ typename Vec<T>::x8 dequant8(uint32_t w0, uint32_t w1, float s,
+                                                       float b) {
+    Dequant8<T, BITS> d;
+    d.init(w0, w1, s, b);
+    return __builtin_bit_cast(typename Vec<T>::x8, (uint4){d.pair(0), d.pair(1), d.pair(2), d.pair(3)});
 }
 
 // Register "launder": an empty asm that claims to rewrite the value. Placed

@@ -883,6 +883,32 @@ __attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<PIPE, A, C>()))) void qmm_m
                         xf[c][u][s] =
                             *(const uint4 *)(cur + (32 * c + r) * 128 + ((chunk ^ swz) << 4));
                     }
+            // Group g = (u * S + s) * A + a is one 32-row x 16-k MFMA operand
+            // and its C MFMAs. 4-bit: group 0 is dequantized here, under the
+            // latency of the x reads, and every later group in slices between
+            // the MFMAs of the group before it (below). 8-bit keeps one
+            // dequant per group ahead of its MFMAs: its dequant is lighter,
+            // and the pipeline's extra live registers made the 128-token dual
+            // tile spill (M = 2048: 335 -> 395 us).
+            constexpr bool PIPED = BITS == 4;
+            typedef Dequant8<T, BITS> Dq;
+            auto dq_init = [&](Dq &d, int g) {
+                const int u = g / (S * A), s = (g / A) % S, a = g % A;
+                const uint32_t words[4] = {wq[a][u].x, wq[a][u].y, wq[a][u].z, wq[a][u].w};
+                d.init(BITS == 4 ? words[s] : words[2 * s], BITS == 4 ? 0u : words[2 * s + 1],
+                       (float)__builtin_bit_cast(T, (uint16_t)sq[a][u]),
+                       (float)__builtin_bit_cast(T, (uint16_t)bq[a][u]));
+            };
+            uint32_t opa[4];  // the next MFMA operand: four packed pairs
+            if constexpr (PIPED) {
+                Dq d;
+                dq_init(d, 0);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    opa[k] = d.pair(k);
+                    launder(opa[k]);  // computed here, not sunk to its MFMA
+                }
+            }
             const int nx = st + Sh::LEAD < last ? st + Sh::LEAD : last;
             if constexpr (Sh::SINGLE) {
                 // the slot's reads have returned before its refill is issued
@@ -896,24 +922,49 @@ __attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<PIPE, A, C>()))) void qmm_m
                 load_w(nx, wreg[(j + 1) % 2]);
             }
             __builtin_amdgcn_sched_barrier(0);
+            // Software pipeline: each MFMA of group g is followed by a slice
+            // of group g + 1's dequant (pair k after MFMA k * C / 4), so one
+            // wave issues its VALU while its MFMAs run. The laundered pairs
+            // and the fences keep instruction selection and the scheduler
+            // from clustering the MFMAs again (they did, four at a time,
+            // leaving the dequant exposed). Each accumulator still receives
+            // its MFMAs in K order: the results do not change.
+            constexpr int NG = SPS * S * A;
 #pragma unroll
-            for (int u = 0; u < SPS; ++u)
+            for (int g = 0; g < NG; ++g) {
+                const int u = g / (S * A), s = (g / A) % S, a = g % A;
+                Dq d;
+                if constexpr (!PIPED) {
+                    dq_init(d, g);
 #pragma unroll
-                for (int s = 0; s < S; ++s)
+                    for (int k = 0; k < 4; ++k) opa[k] = d.pair(k);
+                }
+                const V8 af = __builtin_bit_cast(V8, (uint4){opa[0], opa[1], opa[2], opa[3]});
+                if constexpr (!PIPED) {
 #pragma unroll
-                    for (int a = 0; a < A; ++a) {
-                        const uint32_t words[4] = {wq[a][u].x, wq[a][u].y, wq[a][u].z, wq[a][u].w};
-                        const float sf = (float)__builtin_bit_cast(T, (uint16_t)sq[a][u]);
-                        const float bf = (float)__builtin_bit_cast(T, (uint16_t)bq[a][u]);
-                        const V8 af = (BITS == 4)
-                                          ? dequant8<T, 4>(words[s], 0u, sf, bf)
-                                          : dequant8<T, 8>(words[2 * s], words[2 * s + 1], sf, bf);
+                    for (int c = 0; c < C; ++c)
+                        acc[a][c] = Mfma<T>::mma(af, __builtin_bit_cast(V8, xf[c][u][s]), acc[a][c]);
+                    continue;
+                }
 #pragma unroll
-                        for (int c = 0; c < C; ++c)
-                            acc[a][c] =
-                                Mfma<T>::mma(af, __builtin_bit_cast(V8, xf[c][u][s]), acc[a][c]);
+                for (int c = 0; c < C; ++c) {
+                    acc[a][c] = Mfma<T>::mma(af, __builtin_bit_cast(V8, xf[c][u][s]), acc[a][c]);
+                    if (g + 1 < NG) {
+                        if (c == 0) {
+                            dq_init(d, g + 1);
+                            launder(d.a);
+                            launder(d.b);
+                        }
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            if ((k * C) / 4 == c) {
+                                opa[k] = d.pair(k);
+                                launder(opa[k]);
+                            }
                     }
-            __builtin_amdgcn_sched_barrier(0);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
             load_sb(st < last ? st + 1 : last);
         }
     }
