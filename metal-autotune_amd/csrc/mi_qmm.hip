@@ -56,6 +56,7 @@ struct QParams {
     int gs_log2;               // log2(gs): group sizes are powers of two
     int wk;                    // K-split waves (qmm_mfma_kernel)
     int sbp;                   // qmm_mfma_kernel: groups per row of a wave's scale/bias table
+    int n4;                    // qmm_mfma_mixed_kernel: feature tiles taken as 128-token tiles
 };
 
 template <typename T> __device__ __forceinline__ float swiglu1(float g, float u) {
@@ -655,12 +656,15 @@ template <int PIPE, int A, int C> constexpr int mfma_waves_per_eu() {
     return PIPE == 1 ? (A * C <= 4 && C <= 2 ? 3 : 2) : 1;
 }
 
-template <typename T, int BITS, int A, int C, int WK, int PIPE, int EPI, int WF = 1>
-__global__ __launch_bounds__(64 * WK)
-__attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<PIPE, A, C>()))) void qmm_mfma_kernel(
-    QParams p) {
+// One workgroup's tile: tokens [m_blk, m_blk + 32 * C) of the output features
+// starting at n_blk (32 * TN * WF of them, per part). lds is the workgroup's
+// static LDS, at least MfmaShape::LDS bytes; the scale/bias tables live in
+// the dynamic LDS.
+template <typename T, int BITS, int A, int C, int WK, int PIPE, int EPI, int WF>
+__device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64_t n_blk,
+                                              int64_t m_blk) {
     // The body uses gfx950 buffer resources, which the host target cannot
-    // type; the host pass needs only the launch stub.
+    // type; the host pass needs only the kernels' launch stubs.
 #if defined(__HIP_DEVICE_COMPILE__)
     typedef MfmaShape<T, BITS, A, C, WK, PIPE, WF> Sh;
     constexpr int P = epi_parts(EPI);
@@ -668,7 +672,6 @@ __attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<PIPE, A, C>()))) void qmm_m
     constexpr int TN = (P == 1) ? A : 1;  // 32-wide output tiles per wave
     constexpr int VPW = Sh::VPW, VPC = Sh::VPC, S = Sh::S, SS = Sh::SS, SPS = Sh::SPS;
     typedef typename Vec<T>::x8 V8;
-    __shared__ __attribute__((aligned(16))) char lds[Sh::LDS];
 
     const int lane = threadIdx.x & 63;
     // the wave indices are uniform per wave: in scalar registers, the x stage
@@ -679,9 +682,8 @@ __attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<PIPE, A, C>()))) void qmm_m
     const int fw = wv % WF, kw = wv / WF;
     const int h = lane >> 5, r = lane & 31;
     const int64_t K = p.K, G = K / p.gs;
-    int64_t n_wave = (int64_t)blockIdx.x * (32 * TN * WF) + fw * (32 * TN);
+    int64_t n_wave = n_blk + fw * (32 * TN);
     const Bound bd = bind<EPI>(p, n_wave);
-    const int64_t m_blk = (int64_t)blockIdx.y * (32 * C);
     const int wk = p.wk;
     const int Kw = (int)(K / wk);
     const int kbeg = kw * Kw;
@@ -1042,6 +1044,55 @@ __attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<PIPE, A, C>()))) void qmm_m
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
+template <typename T, int BITS, int A, int C, int WK, int PIPE, int EPI, int WF = 1>
+__global__ __launch_bounds__(64 * WK)
+__attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<PIPE, A, C>()))) void qmm_mfma_kernel(
+    QParams p) {
+    constexpr int TN = (epi_parts(EPI) == 1) ? A : 1;
+    __shared__ __attribute__((aligned(16))) char lds[MfmaShape<T, BITS, A, C, WK, PIPE, WF>::LDS];
+    qmm_mfma_tile<T, BITS, A, C, WK, PIPE, EPI, WF>(p, lds, (int64_t)blockIdx.x * (32 * TN * WF),
+                                                    (int64_t)blockIdx.y * (32 * C));
+}
+
+// Mixed tiles for 64 < M <= 128: workgroups [0, n4) take feature tiles
+// 0..n4-1 with 128-token tiles (all the tokens); the rest take the remaining
+// feature tiles with 64-token tiles, two workgroups each. With n4 chosen so
+// the grid is exactly one or two workgroups per CU, no CU runs one more
+// workgroup than the others, which would finish a whole workgroup later
+// (the M = 128 dual, 608 workgroups of 64 tokens: 32-33 us, against 25 us for
+// 512; mixed: 30.9 us). Tiles never change the results (same K split and
+// accumulation order).
+template <typename T, int BITS, int A, int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qmm_mfma_mixed_kernel(
+    QParams p) {
+    constexpr int TN = (epi_parts(EPI) == 1) ? A : 1;
+    constexpr int L4 = MfmaShape<T, BITS, A, 4, 4, 1>::LDS, L2 = MfmaShape<T, BITS, A, 2, 4, 1>::LDS;
+    __shared__ __attribute__((aligned(16))) char lds[L4 > L2 ? L4 : L2];
+    const int64_t b = blockIdx.x;
+    if (b < p.n4) {
+        qmm_mfma_tile<T, BITS, A, 4, 4, 1, EPI, 1>(p, lds, b * (32 * TN), 0);
+    } else {
+        // The two 64-token workgroups of feature tile n4 + j sit 8 blocks
+        // apart: blocks are dealt to MI355X's 8 XCDs in turn, so both land on
+        // one XCD and the second reads the weight tile from its L2 (adjacent
+        // blocks fetched every weight byte twice from HBM). Groups of 8 tiles
+        // take 16 blocks; a last partial group of r tiles pairs blocks r apart.
+        const int64_t i = b - p.n4;
+        const int64_t n2 = (p.Nout + 32 * TN - 1) / (32 * TN) - p.n4;
+        const int64_t full = 16 * (n2 / 8);
+        int64_t j, half;
+        if (i < full) {
+            j = 8 * (i / 16) + i % 8;
+            half = (i / 8) % 2;
+        } else {
+            const int64_t rem = n2 % 8, t = i - full;
+            j = 8 * (n2 / 8) + t % rem;
+            half = t / rem;
+        }
+        qmm_mfma_tile<T, BITS, A, 2, 4, 1, EPI, 1>(p, lds, (p.n4 + j) * (32 * TN), half * 64);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // dispatch
 
@@ -1087,6 +1138,35 @@ int launch_mfma_cfg(QParams p, int wk, hipStream_t st) {
     return launch_status("quantized matmul (mfma)");
 }
 
+// Compute units of the current device (cached per device).
+int device_cus() {
+    static int cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cache[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cache[dev] = n;
+    }
+    return cache[dev];
+}
+
+// qmm_mfma_mixed_kernel over nt feature tiles, the first n4 of them as
+// 128-token tiles (four K-split waves).
+template <typename T, int BITS, int A, int EPI>
+int launch_mfma_mixed(QParams p, int n4, int64_t nt, hipStream_t st) {
+    p.wk = 4;
+    const SbtLayout tl = sbt_layout(p.K / 4, p.gs);
+    p.sbp = tl.pitch;
+    p.n4 = n4;
+    const size_t dyn = (size_t)4 * A * 2 * tl.array_bytes;
+    const unsigned blocks = (unsigned)(n4 + 2 * (nt - n4));
+    qmm_mfma_mixed_kernel<T, BITS, A, EPI><<<blocks, 256, dyn, st>>>(p);
+    return launch_status("quantized matmul (mfma, mixed tiles)");
+}
+
 // Tile choice (measured on MI355X over the Qwen3 prefill shapes, M = 128): one
 // 32-feature tile per part (A = P) and 64-token tiles (C = 2) -- the smallest
 // tiles that still reuse each x fragment across two MFMA columns -- give the
@@ -1120,6 +1200,20 @@ int launch_mfma(const QParams &p, hipStream_t st) {
     if constexpr (P == 2) {
         if (large && mfma_lds_bytes<T, BITS, 2, 4>(p, wk) <= LDS_PER_CU)
             return launch_mfma_cfg<T, BITS, 2, 4, EPI>(p, wk, st);
+    }
+    // 64 < M <= 128 dual outputs whose 64-token grid puts a third workgroup on
+    // some CUs: mixed tiles make it exactly two per CU, at most one 128-token
+    // tile on each (4-bit; the 8-bit 128-token dual tile spills), when two of
+    // the larger workgroups fit a CU's LDS. (Aiming at one per CU does not
+    // pay: q/k/v at M = 128, 384 -> 256 workgroups, 15.2 -> 15.4 us; a lone
+    // 128-token workgroup takes as long as two 64-token ones sharing a CU.)
+    if constexpr (BITS == 4 && P == 2 && mfma_pipe<T, BITS, P, 4>() == 1 &&
+                  mfma_pipe<T, BITS, P, 2>() == 1) {
+        const int64_t cus = device_cus();
+        const int64_t n4 = 2 * nt - 2 * cus;
+        if (p.M > 64 && p.M <= 128 && wk == 4 && n4 > 0 && n4 <= cus &&
+            2 * mfma_lds_bytes<T, BITS, P, 4>(p, wk) <= LDS_PER_CU)
+            return launch_mfma_mixed<T, BITS, P, EPI>(p, (int)n4, nt, st);
     }
     if (p.M > 32 && nt * ceil_div(p.M, 64) >= 128 &&
         mfma_lds_bytes<T, BITS, P, 2>(p, wk) <= LDS_PER_CU) {

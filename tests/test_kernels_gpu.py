@@ -201,6 +201,37 @@ def test_qmm_dual_and_swiglu(M):
     assert torch.equal(sw, ops.swiglu(g, u))
 
 
+@pytest.mark.parametrize("M,N", [(128, 9728), (100, 9728), (128, 8704)])
+def test_qmm_dual_mixed_tiles_equal_plain_tiles(M, N):
+    """64 < M <= 128 with more 64-token workgroups than two per CU (on
+    MI355X's 256 CUs: N = 9728 gives 608, N = 8704 gives 544) runs the mixed
+    grid: 128-token tiles for the first feature tiles, 64-token pairs after.
+    Tiles never change results, so it equals, bit for bit, rows [0, 64) and
+    [64, M) from two launches of at most 64 rows (the plain 64-token grid);
+    and features at both ends (both tile kinds) are within tolerance of the
+    oracle."""
+    r = rng(760 + M + N)
+    K = 2560
+    x = oracle.round_to(r.normal(0, 1, (1, M, K)), "bfloat16")
+    q1 = _quant(761, N, K)
+    q3 = _quant(762, N, K)
+    xd = to_torch(x, "bfloat16")
+    w = (*_dev(*q1, "bfloat16"), *_dev(*q3, "bfloat16"))
+    lo_x, hi_x = xd[:, :64].contiguous(), xd[:, 64:].contiguous()
+    g, u = ops.qmm_dual(xd, *w)
+    for full, part_lo, part_hi in zip((g, u), ops.qmm_dual(lo_x, *w), ops.qmm_dual(hi_x, *w)):
+        assert torch.equal(full, torch.cat([part_lo, part_hi], dim=1))
+    sw = ops.qmm_dual(xd, *w, swiglu=True)
+    sw_parts = [ops.qmm_dual(part, *w, swiglu=True) for part in (lo_x, hi_x)]
+    assert torch.equal(sw, torch.cat(sw_parts, dim=1))
+    for sl in (slice(0, 256), slice(N - 256, N)):
+        gw = oracle.quantized_matmul(x, *(a[sl] for a in q1), 64, 4, "bfloat16")
+        uw = oracle.quantized_matmul(x, *(a[sl] for a in q3), 64, 4, "bfloat16")
+        _close(g[..., sl], gw, "bfloat16")
+        _close(u[..., sl], uw, "bfloat16")
+        _close(sw[..., sl], oracle.swiglu(gw, uw, "bfloat16"), "bfloat16")
+
+
 @pytest.mark.parametrize("M", [1, 3, 8, 16, 40, 128, 300])
 @pytest.mark.parametrize("bits,dtype", [(4, "bfloat16"), (8, "float16"), (4, "float32")])
 def test_qmm_grouped3_equals_three_launches(M, bits, dtype):
@@ -220,6 +251,28 @@ def test_qmm_grouped3_equals_three_launches(M, bits, dtype):
         assert torch.equal(y, sep)
         _close(y, oracle.quantized_matmul(x, wq, s, b, 64, bits, dtype), dtype,
                1e-5 if dtype == "float32" else None)
+
+
+@pytest.mark.parametrize("M", [128, 72])
+def test_qmm_grouped3_mixed_tiles_qwen3_shape(M):
+    """Qwen3 q/k/v (N 4096 + 1024 + 1024, K 2560) at 64 < M <= 128, where the
+    grouped launch and the three separate launches use different grids: bit
+    for bit equal, and within tolerance of the oracle on the first and last
+    128 features of each part."""
+    r = rng(740 + M)
+    K = 2560
+    Ns = (4096, 1024, 1024)
+    x = oracle.round_to(r.normal(0, 1, (1, M, K)), "bfloat16")
+    qs = [_quant(741 + i, n, K) for i, n in enumerate(Ns)]
+    xd = to_torch(x, "bfloat16")
+    ws = [_dev(*q, "bfloat16") for q in qs]
+    got = ops.qmm_grouped3(xd, ws, 64, 4)
+    for q, w, y in zip(qs, ws, got):
+        assert torch.equal(y, ops.quantized_matmul(xd, *w, group_size=64, bits=4))
+        n = q[0].shape[0]
+        for sl in (slice(0, 128), slice(n - 128, n)):
+            want = oracle.quantized_matmul(x, *(a[sl] for a in q), 64, 4, "bfloat16")
+            _close(y[..., sl], want, "bfloat16")
 
 
 def test_qmm_grouped3_rejects_unaligned_parts():
