@@ -58,6 +58,48 @@ def test_dequant_config2_shape_bit_exact():
     assert np.array_equal(to_np(got).view(np.uint32), want.view(np.uint32))
 
 
+def _onehot_x(M, K, seed):
+    """x rows holding a single 1.0, at column cols[m]: x @ W^T then reads
+    column cols[m] of the dequantized W exactly (one nonzero product, fp32
+    accumulation, a bf16 store of a bf16 value)."""
+    cols = rng(seed).integers(0, K, M)
+    x = np.zeros((1, M, K), np.float32)
+    x[0, np.arange(M), cols] = 1.0
+    return x, cols
+
+
+@pytest.mark.parametrize("M", [16, 128])
+@pytest.mark.parametrize("case", ["quantized", "tiny_bias", "edges"])
+def test_qmm_mfma_dequant_bit_exact_one_hot(M, case):
+    """A1 inside the MFMA GEMM, bit for bit: with one-hot x rows, y[m, n] is
+    W[n, cols[m]] of the dequantized matrix, so every dequantized value the
+    MFMAs consumed is checked against the oracle. 'quantized' groups come from
+    the affine quantizer; 'tiny_bias' groups have b = ±s/1024; 'edges' mixes
+    zero scales, zero biases, negative scales and b/s exponent gaps from 2^-6
+    to 2^22. M = 16 runs 32-token tiles, M = 128 64-token tiles; the dual
+    output runs the register-prefetched two-part tile."""
+    N, K = 2048, 2560
+    wq, s, b = _quant(780, N, K)
+    r = rng(781)
+    if case == "tiny_bias":
+        b = oracle.round_to(s * np.float32(2.0 ** -10) * r.choice([-1, 1], s.shape), "bfloat16")
+    elif case == "edges":
+        pick = r.integers(0, 6, s.shape)
+        gap = np.float32(2.0) ** r.integers(-6, 23, s.shape).astype(np.float32)
+        b_gap = oracle.round_to(np.abs(s) * gap * r.choice([-1, 1], s.shape), "bfloat16")
+        s = np.where(pick == 0, 0.0, np.where(pick == 1, -s, s)).astype(np.float32)
+        b = np.where(pick == 2, 0.0, np.where(pick >= 3, b_gap, b)).astype(np.float32)
+    want = oracle.dequantize(wq, s, b, 64, 4, "bfloat16")
+    x, cols = _onehot_x(M, K, 782 + M)
+    xd = to_torch(x, "bfloat16")
+    w = _dev(wq, s, b, "bfloat16")
+    expect = np.ascontiguousarray(want[:, cols].T)
+    got = to_np(ops.quantized_matmul(xd, *w))[0]
+    assert np.array_equal(got.view(np.uint32), expect.view(np.uint32))
+    for part in ops.qmm_dual(xd, *w, *w):
+        assert np.array_equal(to_np(part)[0].view(np.uint32), expect.view(np.uint32))
+
+
 def test_quantized_embedding_gathers_dequantized_rows():
     wq, s, b = _quant(8, 500, 256)
     W = oracle.dequantize(wq, s, b, 64, 4, "bfloat16")
