@@ -1057,11 +1057,10 @@ __attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<PIPE, A, C>()))) void qmm_m
 // Mixed tiles for 64 < M <= 128: workgroups [0, n4) take feature tiles
 // 0..n4-1 with 128-token tiles (all the tokens); the rest take the remaining
 // feature tiles with 64-token tiles, two workgroups each. With n4 chosen so
-// the grid is exactly one or two workgroups per CU, no CU runs one more
-// workgroup than the others, which would finish a whole workgroup later
-// (the M = 128 dual, 608 workgroups of 64 tokens: 32-33 us, against 25 us for
-// 512; mixed: 30.9 us). Tiles never change the results (same K split and
-// accumulation order).
+// the grid is exactly two workgroups per CU, no CU runs a third workgroup,
+// which would finish a whole workgroup after the rest (the M = 128 dual, 608
+// workgroups of 64 tokens: 32-33 us, against 25 us for 512; mixed: 29.6-30.3
+// us). Tiles never change the results (same K split and accumulation order).
 template <typename T, int BITS, int A, int EPI>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qmm_mfma_mixed_kernel(
     QParams p) {
