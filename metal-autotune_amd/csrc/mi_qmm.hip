@@ -1054,42 +1054,64 @@ __attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<PIPE, A, C>()))) void qmm_m
                                                     (int64_t)blockIdx.y * (32 * C));
 }
 
-// Mixed tiles for 64 < M <= 128: workgroups [0, n4) take feature tiles
-// 0..n4-1 with 128-token tiles (all the tokens); the rest take the remaining
-// feature tiles with 64-token tiles, two workgroups each. With n4 chosen so
-// the grid is exactly two workgroups per CU, no CU runs a third workgroup,
-// which would finish a whole workgroup after the rest (the M = 128 dual, 608
-// workgroups of 64 tokens: 32-33 us, against 25 us for 512; mixed: 29.6-30.3
-// us). Tiles never change the results (same K split and accumulation order).
-template <typename T, int BITS, int A, int EPI>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qmm_mfma_mixed_kernel(
-    QParams p) {
-    constexpr int TN = (epi_parts(EPI) == 1) ? A : 1;
-    constexpr int L4 = MfmaShape<T, BITS, A, 4, 4, 1>::LDS, L2 = MfmaShape<T, BITS, A, 2, 4, 1>::LDS;
-    __shared__ __attribute__((aligned(16))) char lds[L4 > L2 ? L4 : L2];
-    const int64_t b = blockIdx.x;
-    if (b < p.n4) {
-        qmm_mfma_tile<T, BITS, A, 4, 4, 1, EPI, 1>(p, lds, b * (32 * TN), 0);
+// Block i of a run of n feature tiles that take g workgroups each (the g
+// token blocks of a tile): tile j, token block part. A tile's workgroups sit 8
+// blocks apart: blocks are dealt to MI355X's 8 XCDs in turn, so they land on
+// one XCD and all but the first read the weight tile from its L2 (adjacent
+// blocks fetched every weight byte g times from HBM). Groups of 8 tiles take
+// 8 g blocks; a last partial group of r tiles spaces its blocks r apart.
+__device__ __forceinline__ void mixed_tile_of(int64_t i, int64_t n, int g, int64_t &j,
+                                              int64_t &part) {
+    const int64_t full = 8 * g * (n / 8);
+    if (i < full) {
+        j = 8 * (i / (8 * g)) + i % 8;
+        part = (i / 8) % g;
     } else {
-        // The two 64-token workgroups of feature tile n4 + j sit 8 blocks
-        // apart: blocks are dealt to MI355X's 8 XCDs in turn, so both land on
-        // one XCD and the second reads the weight tile from its L2 (adjacent
-        // blocks fetched every weight byte twice from HBM). Groups of 8 tiles
-        // take 16 blocks; a last partial group of r tiles pairs blocks r apart.
-        const int64_t i = b - p.n4;
-        const int64_t n2 = (p.Nout + 32 * TN - 1) / (32 * TN) - p.n4;
-        const int64_t full = 16 * (n2 / 8);
-        int64_t j, half;
-        if (i < full) {
-            j = 8 * (i / 16) + i % 8;
-            half = (i / 8) % 2;
-        } else {
-            const int64_t rem = n2 % 8, t = i - full;
-            j = 8 * (n2 / 8) + t % rem;
-            half = t / rem;
-        }
-        qmm_mfma_tile<T, BITS, A, 2, 4, 1, EPI, 1>(p, lds, (p.n4 + j) * (32 * TN), half * 64);
+        const int64_t rem = n % 8, t = i - full;
+        j = 8 * (n / 8) + t % rem;
+        part = t / rem;
     }
+}
+
+// Mixed tiles for 64 < M <= 128, in two sizes: the first nb feature tiles
+// take CB * 32-token tiles (128/(32 CB) workgroups each), the rest half that
+// (twice the workgroups). With nb chosen so the grid is exactly two
+// workgroups per CU, dealt so that no CU takes two of the larger ones, no CU
+// runs one workgroup more than the others, which would finish a whole
+// workgroup after the rest. Measured at M = 128:
+// - the dual (CB = 4): 608 workgroups of 64 tokens took 32-33 us, against
+//   25 us for 512; mixed, 29.6-30.3 us;
+// - q/k/v (CB = 2): 384 workgroups of 64 tokens, 14.6-15.3 us; mixed with
+//   32-token tiles, 13.2-13.3 us.
+// Tiles never change the results (same K split and accumulation order).
+template <typename T, int BITS, int A, int EPI, int CB>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<1, A, CB>()))) void qmm_mfma_mixed_kernel(
+    QParams p) {
+    static_assert(CB == 4 || CB == 2, "128/64- or 64/32-token tiles");
+    constexpr int CS = CB / 2, GB = 4 / CB, GS = 2 * GB;
+    constexpr int TN = (epi_parts(EPI) == 1) ? A : 1;
+    constexpr int LB = MfmaShape<T, BITS, A, CB, 4, 1>::LDS, LS = MfmaShape<T, BITS, A, CS, 4, 1>::LDS;
+    __shared__ __attribute__((aligned(16))) char lds[LB > LS ? LB : LS];
+    const int64_t b = blockIdx.x, nb = p.n4;
+    const int64_t nt = (p.Nout + 32 * TN - 1) / (32 * TN);
+    int64_t j, part;
+    if constexpr (CB == 4) {
+        // (the 128-token tiles, one block each, written out directly: the
+        // same mapping through mixed_tile_of ran the M = 128 dual at 33.8-34.0
+        // instead of 29.5-29.7 us, A/B on one box, with an identical main
+        // loop; the cause was not found)
+        if (b < nb) {
+            qmm_mfma_tile<T, BITS, A, CB, 4, 1, EPI, 1>(p, lds, b * (32 * TN), 0);
+            return;
+        }
+    } else if (b < nb * GB) {
+        mixed_tile_of(b, nb, GB, j, part);
+        qmm_mfma_tile<T, BITS, A, CB, 4, 1, EPI, 1>(p, lds, j * (32 * TN), part * 32 * CB);
+        return;
+    }
+    mixed_tile_of(b - nb * GB, nt - nb, GS, j, part);
+    qmm_mfma_tile<T, BITS, A, CS, 4, 1, EPI, 1>(p, lds, (nb + j) * (32 * TN), part * 32 * CS);
 }
 
 // ---------------------------------------------------------------------------
@@ -1152,17 +1174,17 @@ int device_cus() {
     return cache[dev];
 }
 
-// qmm_mfma_mixed_kernel over nt feature tiles, the first n4 of them as
-// 128-token tiles (four K-split waves).
-template <typename T, int BITS, int A, int EPI>
-int launch_mfma_mixed(QParams p, int n4, int64_t nt, hipStream_t st) {
+// qmm_mfma_mixed_kernel over nt feature tiles, the first nb of them as
+// CB * 32-token tiles (four K-split waves).
+template <typename T, int BITS, int A, int EPI, int CB>
+int launch_mfma_mixed(QParams p, int nb, int64_t nt, hipStream_t st) {
     p.wk = 4;
     const SbtLayout tl = sbt_layout(p.K / 4, p.gs);
     p.sbp = tl.pitch;
-    p.n4 = n4;
+    p.n4 = nb;
     const size_t dyn = (size_t)4 * A * 2 * tl.array_bytes;
-    const unsigned blocks = (unsigned)(n4 + 2 * (nt - n4));
-    qmm_mfma_mixed_kernel<T, BITS, A, EPI><<<blocks, 256, dyn, st>>>(p);
+    const unsigned blocks = (unsigned)(nb * (4 / CB) + (nt - nb) * (8 / CB));
+    qmm_mfma_mixed_kernel<T, BITS, A, EPI, CB><<<blocks, 256, dyn, st>>>(p);
     return launch_status("quantized matmul (mfma, mixed tiles)");
 }
 
@@ -1200,19 +1222,28 @@ int launch_mfma(const QParams &p, hipStream_t st) {
         if (large && mfma_lds_bytes<T, BITS, 2, 4>(p, wk) <= LDS_PER_CU)
             return launch_mfma_cfg<T, BITS, 2, 4, EPI>(p, wk, st);
     }
-    // 64 < M <= 128 dual outputs whose 64-token grid puts a third workgroup on
-    // some CUs: mixed tiles make it exactly two per CU, at most one 128-token
-    // tile on each (4-bit; the 8-bit 128-token dual tile spills), when two of
-    // the larger workgroups fit a CU's LDS. (Aiming at one per CU does not
-    // pay: q/k/v at M = 128, 384 -> 256 workgroups, 15.2 -> 15.4 us; a lone
-    // 128-token workgroup takes as long as two 64-token ones sharing a CU.)
-    if constexpr (BITS == 4 && P == 2 && mfma_pipe<T, BITS, P, 4>() == 1 &&
-                  mfma_pipe<T, BITS, P, 2>() == 1) {
+    // 64 < M <= 128 whose 64-token grid (2 nt workgroups) puts one workgroup
+    // more on some CUs than on others: mixed tiles make it exactly two per CU,
+    // at most one of the larger workgroups on each, when two of them fit a
+    // CU's LDS (4-bit; the 8-bit 128-token dual tile spills).
+    // - more than two per CU (dual outputs): 128/64-token tiles;
+    // - between one and one and a half per CU: 64/32-token tiles.
+    // Aiming at one per CU does not pay: q/k/v at M = 128 with 128/64-token
+    // tiles, 384 -> 256 workgroups, went 15.2 -> 15.4 us; a lone larger
+    // workgroup takes as long as two smaller ones sharing a CU.
+    if constexpr (BITS == 4 && P <= 2 && mfma_pipe<T, BITS, P, 4>() == 1 &&
+                  mfma_pipe<T, BITS, P, 2>() == 1 && mfma_pipe<T, BITS, P, 1>() == 1) {
         const int64_t cus = device_cus();
-        const int64_t n4 = 2 * nt - 2 * cus;
-        if (p.M > 64 && p.M <= 128 && wk == 4 && n4 > 0 && n4 <= cus &&
-            2 * mfma_lds_bytes<T, BITS, P, 4>(p, wk) <= LDS_PER_CU)
-            return launch_mfma_mixed<T, BITS, P, EPI>(p, (int)n4, nt, st);
+        if (p.M > 64 && p.M <= 128 && wk == 4) {
+            if constexpr (P == 2) {
+                const int64_t nb4 = 2 * nt - 2 * cus;  // 128-token tiles
+                if (nb4 > 0 && nb4 <= cus && 2 * mfma_lds_bytes<T, BITS, P, 4>(p, wk) <= LDS_PER_CU)
+                    return launch_mfma_mixed<T, BITS, P, EPI, 4>(p, (int)nb4, nt, st);
+            }
+            const int64_t nb2 = 2 * nt - cus;  // 64-token tiles (two blocks each)
+            if (nb2 > 0 && 2 * nb2 <= cus && 2 * mfma_lds_bytes<T, BITS, P, 2>(p, wk) <= LDS_PER_CU)
+                return launch_mfma_mixed<T, BITS, P, EPI, 2>(p, (int)nb2, nt, st);
+        }
     }
     if (p.M > 32 && nt * ceil_div(p.M, 64) >= 128 &&
         mfma_lds_bytes<T, BITS, P, 2>(p, wk) <= LDS_PER_CU) {
