@@ -243,15 +243,16 @@ def test_qmm_dual_and_swiglu(M):
     assert torch.equal(sw, ops.swiglu(g, u))
 
 
-@pytest.mark.parametrize("M,N", [(128, 9728), (100, 9728), (128, 8704)])
+@pytest.mark.parametrize("M,N", [(128, 9728), (100, 9728), (128, 8704), (128, 5120)])
 def test_qmm_dual_mixed_tiles_equal_plain_tiles(M, N):
-    """64 < M <= 128 with more 64-token workgroups than two per CU (on
-    MI355X's 256 CUs: N = 9728 gives 608, N = 8704 gives 544) runs the mixed
-    grid: 128-token tiles for the first feature tiles, 64-token pairs after.
-    Tiles never change results, so it equals, bit for bit, rows [0, 64) and
-    [64, M) from two launches of at most 64 rows (the plain 64-token grid);
-    and features at both ends (both tile kinds) are within tolerance of the
-    oracle."""
+    """64 < M <= 128 whose 64-token grid puts one workgroup more on some CUs
+    runs a mixed grid. On MI355X's 256 CUs, N = 9728 (608 workgroups) and
+    N = 8704 (544) take 128-token tiles for the first feature tiles and
+    64-token pairs after; N = 5120 (320) takes 64-token pairs and 32-token
+    quads. Tiles never change results, so it equals, bit for bit, rows
+    [0, 64) and [64, M) from two launches of at most 64 rows (the plain
+    64-token grid); and features at both ends (both tile kinds) are within
+    tolerance of the oracle."""
     r = rng(760 + M + N)
     K = 2560
     x = oracle.round_to(r.normal(0, 1, (1, M, K)), "bfloat16")
