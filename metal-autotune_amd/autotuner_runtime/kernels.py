@@ -36,11 +36,10 @@ synchronize the host.
 
 from __future__ import annotations
 
-import importlib
 import json
+from collections import OrderedDict
 from dataclasses import asdict, dataclass
 from pathlib import Path
-from typing import NamedTuple
 
 import torch
 
@@ -128,16 +127,23 @@ def load_spec(path: str | Path) -> KernelSpec:
     return KernelSpec.from_json(json.dumps(launch))
 
 
-class Launch(NamedTuple):
-    """One call signature's launch, or the fact that the fallback covers it."""
+@dataclass(frozen=True)
+class Launch:
+    """The resolved launch of one call signature.
+
+    ``fallback`` true: the spec does not cover these shapes and the caller's
+    original ops run. Otherwise the evaluated output shapes, the (validated,
+    unused) grid / threadgroup, and the entry point's scalar arguments."""
     fallback: bool
-    output_shapes: list | None = None
-    grid: tuple | None = None
-    threadgroup: tuple | None = None
-    template: list | None = None
+    output_shapes: tuple = ()
+    grid: tuple = ()
+    threadgroup: tuple = ()
+    template: tuple = ()
 
 
-LAUNCH_CACHE_MAX = 64  # signatures kept per kernel; a shape sweep needs a handful
+# Resolved signatures kept per kernel, least recently used dropped first. A
+# wrapper serving a range of prompt lengths sees one signature per length.
+LAUNCH_CACHE_MAX = 64
 
 
 def _template_value(value: str, inputs):
@@ -155,139 +161,155 @@ def _template_value(value: str, inputs):
         raise ValueError(f"template value {value!r} is not a dtype, inK or a number") from None
 
 
+def _signature(inputs) -> list:
+    """The recorded-signature form of a call: [[shape list, dtype name], ...]."""
+    return [[list(a.shape), dtype_name(a.dtype)] for a in inputs]
+
+
 class LoadedKernel:
-    """A spec bound to its HIP entry point plus its parsed launch expressions."""
+    """A spec bound to its HIP entry point (or its stages), with the launch
+    expressions parsed once."""
 
     def __init__(self, spec: KernelSpec):
         from . import hip  # the backend; imported lazily so grammar-only use needs no GPU
 
         self.spec = spec
-        if spec.reference_sequence is not None:
-            raise ValueError(f"kernel {spec.kernel_id}: reference sequences replay MLX ops; "
-                             "the HIP backend runs kernels only")
-        if spec.native_call is not None:
-            raise ValueError(f"kernel {spec.kernel_id}: native_call binds a captured Metal ABI")
-        if spec.atomic_outputs:
-            raise ValueError(f"kernel {spec.kernel_id}: atomic outputs are not part of this ABI")
+        for field_name, what in (("reference_sequence", "replays MLX ops"),
+                                 ("native_call", "binds a captured Metal ABI"),
+                                 ("atomic_outputs", "asks for Metal atomic outputs")):
+            if getattr(spec, field_name) not in (None, False):
+                raise ValueError(f"kernel {spec.kernel_id}: {field_name} {what}; the HIP "
+                                 "backend runs its own entry points only")
         self._stages = None
+        self._entry = None
         if spec.stages:
             from .stages import wiring
-            indices, self._stage_outputs = wiring(spec)
-            self._stages = [(LoadedKernel(stage.kernel), idx)
-                            for stage, idx in zip(spec.stages, indices)]
-            self._entry = None
+            reads, self._stage_outputs = wiring(spec)
+            self._stages = [(LoadedKernel(st.kernel), pos) for st, pos in zip(spec.stages, reads)]
         else:
             self._entry = hip.binding(spec.source)  # unknown entry -> RuntimeError (a build error)
-        self._grid = tuple(Expr(e) for e in spec.grid)
-        self._tg = tuple(Expr(e) for e in spec.threadgroup)
-        self._out_shapes = tuple(tuple(Expr(e) for e in s) for s in spec.output_shapes)
-        self._out_dtypes = [_DTYPES[d] for d in spec.output_dtypes]
         self._fallback = Expr(spec.fallback_predicate) if spec.fallback_predicate else None
-        self._launches: dict[tuple, Launch] = {}
+        self._grid = [Expr(e) for e in spec.grid]
+        self._tg = [Expr(e) for e in spec.threadgroup]
+        self._out_shapes = [[Expr(e) for e in shape] for shape in spec.output_shapes]
+        self._out_dtypes = [_DTYPES[d] for d in spec.output_dtypes]
+        self._launches: OrderedDict[tuple, Launch] = OrderedDict()
+
+    def _uncovered(self, inputs, shapes, checked_elsewhere: bool) -> bool:
+        """True when the original ops must take this call. Decided before any
+        launch expression is evaluated: grid arithmetic may be undefined on
+        the shapes the predicate excludes."""
+        spec = self.spec
+        if not checked_elsewhere and (spec.input_signature is not None
+                                      or spec.input_signatures is not None):
+            sig = _signature(inputs)
+            if spec.input_signature is not None and sig != spec.input_signature:
+                return True
+            if spec.input_signatures is not None and sig not in spec.input_signatures:
+                return True
+        return self._fallback is not None and bool(self._fallback.evaluate(shapes))
+
+    def _resolve(self, inputs, shapes, checked_elsewhere: bool) -> Launch:
+        if self._uncovered(inputs, shapes, checked_elsewhere):
+            return Launch(fallback=True)
+        ev = lambda exprs: tuple(int(e.evaluate(shapes)) for e in exprs)  # noqa: E731
+        grid, tg = ev(self._grid), ev(self._tg)
+        if min(grid + tg) <= 0:
+            raise ValueError(f"kernel {self.spec.kernel_id}: non-positive launch {grid} {tg}")
+        out_shapes = tuple(ev(s) for s in self._out_shapes)
+        if self._stages is not None:
+            from .stages import shapes as stage_shapes
+            _, results = stage_shapes(self.spec, shapes, [dtype_name(a.dtype) for a in inputs])
+            if results != list(zip(out_shapes, self.spec.output_dtypes)):
+                raise ValueError(f"kernel {self.spec.kernel_id}: the stages produce {results}, "
+                                 "not the region's declared output shapes/dtypes")
+        scalars = tuple((name, _template_value(v, inputs)) for name, v in self.spec.template)
+        return Launch(False, out_shapes, grid, tg, scalars)
 
     def launch(self, inputs: list[torch.Tensor], checked_elsewhere: bool = False) -> Launch:
-        """checked_elsewhere: the caller serves only sizes it checked this kernel
-        at, so recorded signatures do not bound the call; the fallback
-        predicate still does."""
-        key = (checked_elsewhere, *((tuple(a.shape), a.dtype) for a in inputs))
-        launch = self._launches.get(key)
-        if launch is not None:
-            return launch
-        shapes = [shape for shape, _ in key[1:]]
-        spec = self.spec
-        signature = [[list(a.shape), dtype_name(a.dtype)] for a in inputs]
-        if ((not checked_elsewhere and (
-                (spec.input_signature is not None and signature != spec.input_signature)
-                or (spec.input_signatures is not None and signature not in spec.input_signatures)))
-                or (self._fallback is not None and self._fallback.evaluate(shapes))):
-            launch = Launch(fallback=True)
-        else:
-            template = [(name, _template_value(v, inputs)) for name, v in spec.template]
-            launch = Launch(
-                fallback=False,
-                output_shapes=[tuple(int(e.evaluate(shapes)) for e in s) for s in self._out_shapes],
-                grid=tuple(int(e.evaluate(shapes)) for e in self._grid),
-                threadgroup=tuple(int(e.evaluate(shapes)) for e in self._tg),
-                template=template,
-            )
-            if any(g <= 0 for g in launch.grid + launch.threadgroup):
-                raise ValueError(f"kernel {spec.kernel_id}: non-positive launch {launch.grid} "
-                                 f"{launch.threadgroup}")
-            if self._stages is not None:
-                from .stages import shapes as stage_shapes
-                _, outs = stage_shapes(spec, shapes, [dtype_name(d) for _, d in key[1:]])
-                if outs != list(zip(launch.output_shapes, spec.output_dtypes)):
-                    raise ValueError("stage results do not match the candidate's output shapes/dtypes")
-        if len(self._launches) >= LAUNCH_CACHE_MAX:
-            self._launches.clear()
-        self._launches[key] = launch
-        return launch
+        """The launch for these inputs' shapes and dtypes, resolved once per
+        signature. ``checked_elsewhere``: a size-generic caller that serves
+        only sizes this kernel was checked at; recorded signatures then do not
+        restrict the call (the fallback predicate still does)."""
+        key = (checked_elsewhere,) + tuple((tuple(a.shape), a.dtype) for a in inputs)
+        hit = self._launches.get(key)
+        if hit is not None:
+            self._launches.move_to_end(key)
+            return hit
+        resolved = self._resolve(inputs, [tuple(a.shape) for a in inputs], checked_elsewhere)
+        self._launches[key] = resolved
+        while len(self._launches) > LAUNCH_CACHE_MAX:
+            self._launches.popitem(last=False)
+        return resolved
 
     def fallback_fires(self, inputs: list[torch.Tensor]) -> bool:
         return self.launch(inputs).fallback
 
+    def _allocate(self, launch: Launch, device, init_value):
+        if init_value is None:
+            return [torch.empty(s, dtype=d, device=device)
+                    for s, d in zip(launch.output_shapes, self._out_dtypes)]
+        return [torch.full(s, init_value, dtype=d, device=device)
+                for s, d in zip(launch.output_shapes, self._out_dtypes)]
+
     def __call__(self, inputs: list[torch.Tensor], init_value: float | None = None,
                  launch: Launch | None = None) -> list[torch.Tensor]:
-        launch = launch or self.launch(inputs)
+        launch = launch if launch is not None else self.launch(inputs)
         if launch.fallback:
-            raise ValueError(f"kernel {self.spec.kernel_id}: these shapes are the fallback's; "
-                             "the original ops take them")
+            raise ValueError(f"kernel {self.spec.kernel_id}: the fallback predicate covers "
+                             "these shapes; the original ops must run them")
         if self.spec.ensure_row_contiguous:
             inputs = [a.contiguous() for a in inputs]
         if self._stages is not None:
-            buffers = list(inputs)
-            for kernel, idx in self._stages:
-                buffers.extend(kernel([buffers[i] for i in idx], init_value=init_value))
-            return [buffers[i] for i in self._stage_outputs]
-        device = inputs[0].device
-        outputs = []
-        for shape, dtype in zip(launch.output_shapes, self._out_dtypes):
-            if init_value is None:
-                outputs.append(torch.empty(shape, dtype=dtype, device=device))
-            else:
-                outputs.append(torch.full(shape, init_value, dtype=dtype, device=device))
+            table = list(inputs)
+            for kernel, pos in self._stages:
+                table += kernel([table[j] for j in pos], init_value=init_value)
+            return [table[j] for j in self._stage_outputs]
+        outputs = self._allocate(launch, inputs[0].device, init_value)
         self._entry(inputs, outputs, dict(launch.template))
         return outputs
-
-
-def imported(path: str):
-    """A callable found by its import path (the reference's kernels.imported)."""
-    module, _, name = path.rpartition(".")
-    return getattr(importlib.import_module(module), name)
 
 
 _cache: dict[str, LoadedKernel] = {}
 
 
-def _loaded(spec: KernelSpec) -> LoadedKernel:
-    loaded = _cache.get(spec.kernel_id)
-    if loaded is None or loaded.spec is not spec:
-        loaded = LoadedKernel(spec)
-        _cache[spec.kernel_id] = loaded
-    return loaded
+def _kernel_for(spec: KernelSpec) -> LoadedKernel:
+    """The loaded kernel of ``spec``, rebuilt when a different spec object
+    arrives under a known id."""
+    lk = _cache.get(spec.kernel_id)
+    if lk is None or lk.spec is not spec:
+        lk = _cache[spec.kernel_id] = LoadedKernel(spec)
+    return lk
+
+
+def _covered_call(spec, inputs, sized: bool, init_value):
+    lk = _kernel_for(spec)
+    plan = lk.launch(inputs, checked_elsewhere=sized)
+    if plan.fallback:
+        return None
+    return lk(inputs, init_value=init_value, launch=plan)
 
 
 def fallback_fires(spec: KernelSpec, inputs: list[torch.Tensor]) -> bool:
-    """True when this call's shapes are not covered and the wrapper must take
-    the original op sequence instead."""
-    return _loaded(spec).fallback_fires(inputs)
+    """Whether the region's original ops must run these inputs."""
+    return _kernel_for(spec).fallback_fires(inputs)
 
 
 def call(spec: KernelSpec, inputs: list[torch.Tensor], init_value: float | None = None,
          launch: Launch | None = None) -> list[torch.Tensor]:
-    """The replacement call site: every dispatch of the region, in order."""
-    return _loaded(spec)(inputs, init_value=init_value, launch=launch)
+    """Run the region (all its launches) and return its outputs; ValueError on
+    shapes the fallback covers."""
+    return _kernel_for(spec)(inputs, init_value=init_value, launch=launch)
 
 
 def try_call(spec: KernelSpec, inputs: list[torch.Tensor]) -> list[torch.Tensor] | None:
-    """The kernel's outputs, or None when the fallback covers these shapes."""
-    launch = _loaded(spec).launch(inputs)
-    return None if launch.fallback else call(spec, inputs, launch=launch)
+    """The region's outputs, or None for shapes (or unrecorded signatures) the
+    original ops take."""
+    return _covered_call(spec, inputs, False, None)
 
 
 def try_sized(spec: KernelSpec, inputs: list[torch.Tensor],
               init_value: float | None = None) -> list[torch.Tensor] | None:
-    """try_call for a size-generic wrapper: recorded signatures do not bound the
-    call, the fallback predicate still does."""
-    launch = _loaded(spec).launch(inputs, checked_elsewhere=True)
-    return None if launch.fallback else call(spec, inputs, init_value=init_value, launch=launch)
+    """As ``try_call`` for callers that gate sizes themselves: only the fallback
+    predicate can decline the call."""
+    return _covered_call(spec, inputs, True, init_value)

@@ -7,8 +7,8 @@ Same policy as the reference's numeric.py:1-122, on torch tensors:
   first; non-float outputs (indices, packed words) must match exactly
   whatever the tolerance; then the non-finite pattern (finite where finite,
   NaN where NaN, same signed inf where inf); then elementwise
-  ``|c - r| <= max(atol + rtol*|r|, wobble_floor)`` in float32 with an
-  overflow-safe excess, failing closed on a NaN error;
+  ``|c - r| <= max(atol + rtol*|r|, wobble_floor)``, evaluated in float64
+  (exact differences, no overflow), failing closed on a NaN error;
 * ``tolerance_for(dtype)`` gives the per-dtype defaults
   (fp32 (1e-5, 1e-6), fp16 (1e-2, 2e-2), bf16 (2e-2, 4e-2)).
 
@@ -68,10 +68,11 @@ class CompareResult:
 
 
 def nonfinite_pattern_ok(c: torch.Tensor, r: torch.Tensor) -> torch.Tensor:
-    finite_ok = torch.isfinite(r) & torch.isfinite(c)
-    nan_ok = torch.isnan(r) & torch.isnan(c)
-    inf_ok = torch.isinf(r) & (c == r)
-    return finite_ok | nan_ok | inf_ok
+    """Per element: where the reference is finite the candidate must be
+    finite, where it is NaN the candidate must be NaN, and where it is an
+    infinity the candidate must be that same infinity."""
+    return torch.where(torch.isfinite(r), torch.isfinite(c),
+                       torch.where(torch.isnan(r), torch.isnan(c), c == r))
 
 
 def _unravel(flat: int, shape: tuple) -> tuple:
@@ -92,64 +93,71 @@ def _worst(excess: torch.Tensor) -> float:
     return float(excess.max())
 
 
+def _same_structure(candidate, reference, distance) -> CompareResult | None:
+    """A failed result when shape or dtype differ, else None."""
+    cs, rs = tuple(candidate.shape), tuple(reference.shape)
+    if cs != rs:
+        return CompareResult(False, "shape", distance, None, f"shape {cs} != {rs}")
+    if candidate.dtype != reference.dtype:
+        return CompareResult(False, "dtype", distance, None,
+                             f"dtype {candidate.dtype} != {reference.dtype}")
+    return None
+
+
 def compare(candidate: torch.Tensor, reference: torch.Tensor, rtol: float, atol: float,
             wobble_floor: float = 0.0) -> CompareResult:
+    """Tolerance comparison: per element |c - r| <= max(atol + rtol*|r|,
+    wobble_floor) after the non-finite pattern rule.
+
+    The float32 values are compared in float64, where their difference is
+    exact and cannot overflow (3e38 against -3e38 is a distance of 6e38, not
+    an infinity that a huge tolerance might absorb). Integer and boolean
+    outputs must be equal whatever the tolerance."""
     validate_tolerances((rtol, atol))
-    if tuple(candidate.shape) != tuple(reference.shape):
-        return CompareResult(False, "shape", float("inf"), None,
-                             f"{tuple(candidate.shape)} != {tuple(reference.shape)}")
-    if candidate.dtype != reference.dtype:
-        return CompareResult(False, "dtype", float("inf"), None,
-                             f"{candidate.dtype} != {reference.dtype}")
+    bad = _same_structure(candidate, reference, float("inf"))
+    if bad is not None:
+        return bad
     if candidate.numel() == 0:
         return CompareResult(True, "", 0.0, None)
-    candidate = candidate.detach()
-    reference = reference.detach().to(candidate.device)
-    if reference.dtype not in FLOAT_DTYPES:
-        # exact values: a float32 conversion could hide a one-unit change above 2**24
-        diff = candidate != reference
-        if bool(diff.any()):
-            return CompareResult(False, "tolerance", float("inf"), _first(diff),
-                                 "non-floating outputs must match exactly")
+    cand = candidate.detach()
+    ref = reference.detach().to(cand.device)
+    if ref.dtype not in FLOAT_DTYPES:
+        differs = cand != ref
+        if bool(differs.any()):
+            return CompareResult(False, "tolerance", float("inf"), _first(differs),
+                                 "integer/boolean outputs must be equal; tolerances do not apply")
         return CompareResult(True, "", 0.0, None)
-    c = candidate.float()
-    r = reference.float()
-    ok = nonfinite_pattern_ok(c, r)
-    if not bool(ok.all()):
-        viol = ~ok
-        return CompareResult(False, "nonfinite_pattern", float("inf"), _first(viol),
-                             f"{int(viol.sum())} elements break the non-finite pattern")
+    c = cand.to(torch.float64)
+    r = ref.to(torch.float64)
+    broken = ~nonfinite_pattern_ok(c, r)
+    if bool(broken.any()):
+        return CompareResult(False, "nonfinite_pattern", float("inf"), _first(broken),
+                             f"{int(broken.sum())} elements break the non-finite pattern")
     finite = torch.isfinite(r)
-    allowed = torch.clamp(atol + rtol * r.abs(), min=wobble_floor)
-    excess = torch.where(finite, (c - r).abs() - allowed, torch.zeros_like(r))
-    # opposite extreme values overflow the subtraction: recompute scaled
-    scale = torch.clamp(torch.maximum(c.abs(), r.abs()), min=1.0)
-    scaled = ((c / scale - r / scale).abs() - (atol / scale + rtol * (r / scale).abs())) * scale
-    bad = finite & (torch.isnan(excess) | torch.isinf(excess))
-    excess = torch.where(bad, scaled, excess)
+    budget = torch.clamp(atol + rtol * r.abs(), min=wobble_floor)
+    excess = torch.where(finite, (c - r).abs() - budget, torch.zeros_like(r))
     worst = _worst(excess)
     if math.isnan(worst):
         return CompareResult(False, "nonfinite_error", None, None,
-                             "comparison produced a NaN error")
+                             "the comparison itself produced a NaN")
     index = _unravel(int(excess.reshape(-1).argmax()), tuple(r.shape))
     if worst > 0:
-        over = int((excess > 0).sum())
-        return CompareResult(False, "tolerance", worst, index, f"{over} elements over tolerance")
+        return CompareResult(False, "tolerance", worst, index,
+                             f"{int((excess > 0).sum())} elements over tolerance")
     return CompareResult(True, "", worst, index)
 
 
 def check(candidate, reference, *, exact=True, rtol=0.0, atol=0.0) -> CompareResult:
-    """Exact by default; tolerance is opt-in for floating evaluation changes."""
+    """The verdict for one output: bit for bit unless ``exact=False``, which
+    applies ``compare`` with (rtol, atol)."""
     if not exact:
         return compare(candidate, reference, rtol, atol)
-    if tuple(candidate.shape) != tuple(reference.shape):
-        return CompareResult(False, "shape", None, None, "output shape changed")
-    if candidate.dtype != reference.dtype:
-        return CompareResult(False, "dtype", None, None, "output dtype changed")
-    if not bitwise_equal(candidate, reference.to(candidate.device)):
-        return CompareResult(False, "exact", None, None,
-                             "output must match the original bit-for-bit")
-    return CompareResult(True, "", 0.0, None)
+    bad = _same_structure(candidate, reference, None)
+    if bad is not None:
+        return bad
+    if bitwise_equal(candidate, reference.to(candidate.device)):
+        return CompareResult(True, "", 0.0, None)
+    return CompareResult(False, "exact", None, None, "bits differ from the original output")
 
 
 @dataclass(frozen=True)

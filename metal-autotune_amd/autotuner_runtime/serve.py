@@ -24,6 +24,7 @@ check and the range:
 
 from __future__ import annotations
 
+import itertools
 import statistics
 
 import torch
@@ -35,26 +36,25 @@ SIZE_NAME = "_n"
 
 
 def runs(sizes) -> list[list[int]]:
-    """Sorted distinct sizes as contiguous [first, last] runs."""
-    out: list[list[int]] = []
-    for n in sorted(set(int(s) for s in sizes)):
-        if out and out[-1][1] == n - 1:
-            out[-1][1] = n
-        else:
-            out.append([n, n])
-    return out
+    """Distinct sizes grouped into consecutive [first, last] runs, ascending.
+    (Consecutive integers share n - rank, which is what groups them.)"""
+    ordered = sorted({int(s) for s in sizes})
+    return [[grp[0][1], grp[-1][1]]
+            for _, grp in ((k, list(g)) for k, g in
+                           itertools.groupby(enumerate(ordered), key=lambda t: t[1] - t[0]))]
 
 
 def size_test(sizes, name: str = SIZE_NAME) -> str:
-    """Python source testing a size against a set: a range for one run, else
-    membership in the exact sizes."""
-    parts = runs(sizes)
-    if not parts:
+    """A Python expression over ``name`` that holds exactly for ``sizes``:
+    an equality or a chained comparison for one run, else a membership test."""
+    spans = runs(sizes)
+    if not spans:
         return "False"
-    if len(parts) == 1:
-        lo, hi = parts[0]
-        return f"{name} == {lo}" if lo == hi else f"{lo} <= {name} <= {hi}"
-    return f"{name} in {tuple(n for lo, hi in parts for n in range(lo, hi + 1))!r}"
+    if len(spans) > 1:
+        members = tuple(n for lo, hi in spans for n in range(lo, hi + 1))
+        return f"{name} in {members!r}"
+    lo, hi = spans[0]
+    return f"{name} == {lo}" if lo == hi else f"{lo} <= {name} <= {hi}"
 
 
 def in_runs(n: int, ranges) -> bool:
@@ -62,32 +62,37 @@ def in_runs(n: int, ranges) -> bool:
 
 
 def served_range(correct, clock: dict, primary: int, grid=None):
-    """(lo, hi) served around ``primary``, or None when the primary is not
-    a correct, non-losing size. ``clock`` maps a timed size to
-    {"win": bool, "loss": bool}; sizes of ``grid`` (default: every timed
-    size) stop the range when not won, other timed sizes only extend it when
-    won (a tie neither extends nor stops it). The primary counts as won."""
+    """The (lo, hi) of sizes a kernel is served at around ``primary``, or
+    None when ``primary`` is itself not servable.
+
+    Servable sizes are the correct ones that were not timed as a loss. From
+    the contiguous servable run around the primary, each side keeps the
+    sizes out to its furthest timed win that lies before the first ``grid``
+    size on that side it does not win at. ``clock`` maps timed sizes to
+    {"win": bool, "loss": bool}; ``grid`` defaults to every timed size, and a
+    timed size outside it that does not win is ignored. The primary counts as
+    a win."""
     grid = set(clock) if grid is None else set(grid)
-    ok = set(correct) - {n for n, row in clock.items() if row.get("loss")}
-    if primary not in ok:
+    lost = {n for n, t in clock.items() if t.get("loss")}
+    servable = set(correct) - lost
+    if primary not in servable:
         return None
     lo = hi = primary
-    while lo - 1 in ok:
+    while lo - 1 in servable:
         lo -= 1
-    while hi + 1 in ok:
+    while hi + 1 in servable:
         hi += 1
-    ends = []
-    for side in (sorted((n for n in clock if lo <= n < primary), reverse=True),
-                 sorted(n for n in clock if primary < n <= hi)):
-        end = primary
-        for n in side:
-            row = clock[n]
-            if row.get("win"):
-                end = n
-            elif n in grid:
-                break
-        ends.append(end)
-    return ends[0], ends[1]
+    won = {n for n, t in clock.items() if t.get("win")}
+    blocked = {n for n in clock if n in grid and n not in won}
+
+    def reach(side: int) -> int:
+        inside = (lambda n: primary < n <= hi) if side > 0 else (lambda n: lo <= n < primary)
+        dist = lambda n: (n - primary) * side  # noqa: E731
+        stop = min((dist(n) for n in blocked if inside(n)), default=None)
+        ok = [n for n in won if inside(n) and (stop is None or dist(n) < stop)]
+        return max(ok, key=dist, default=primary)
+
+    return reach(-1), reach(+1)
 
 
 class SizedRegions(ReplayWrapper):

@@ -1,143 +1,146 @@
-"""Module swap on live torch models (the reference's swap.py:1-152).
+"""Installing region wrappers into live torch models.
 
-Scope addresses are dot paths, used for serialization only: the swap always
-happens on live instances by parent attribute assignment, or index/key
-assignment for children in ``nn.ModuleList`` / lists / dicts. Wrappers are
-``nn.Module`` subclasses so the wrapped subtree stays visible to
-``parameters()`` and ``named_modules()``; attribute lookups a wrapper does not
-define fall through to the wrapped module.
+The drop-in interface of the reference's autotuner_runtime/swap.py (install,
+uninstall, resolve, ReplayWrapper; swap.py:67-152): an artifact's swap table
+names each wrapped scope by a dot path (``model.layers.3.mlp``), and apply()
+puts a wrapper instance in that place. The walk here is this build's own:
+
+* a path is split once into steps; each step is an attribute name, a
+  ``nn.ModuleList`` / list position, or a ``nn.ModuleDict`` / dict key,
+  decided by the container's type (``_Step``);
+* ``install`` returns what was there, and ``uninstall`` puts it back, so a
+  caller can roll a swap back;
+* wrappers are ``nn.Module`` subclasses holding the original as ``wrapped``,
+  so ``parameters()`` still reaches the original weights, and attribute
+  reads the wrapper does not answer go to the original.
 """
 
 from __future__ import annotations
 
+from typing import Any, Iterator
+
 import torch
 from torch import nn
 
-
-def flatten_arrays(tree: object) -> list[torch.Tensor]:
-    """Every tensor of a nested list/tuple/dict tree, in order (iterative walk)."""
-    out: list[torch.Tensor] = []
-    stack = [tree]
-    while stack:
-        obj = stack.pop()
-        if isinstance(obj, torch.Tensor):
-            out.append(obj)
-        elif isinstance(obj, (list, tuple)):
-            stack.extend(reversed(obj))
-        elif isinstance(obj, dict):
-            stack.extend(reversed(list(obj.values())))
-    return out
+_INDEXED = (list, tuple, nn.ModuleList, nn.Sequential)
+_KEYED = (dict, nn.ModuleDict)
 
 
-def state_signature(value):
-    """Structure, scalar settings and tensor shapes of a state object, never its
-    data: guards replays whose control flow depended on a cache's layout."""
-    seen: dict[int, int] = {}
+class _Step:
+    """One component of a scope path, bound to the object it is taken from."""
 
-    def visit(obj):
-        if isinstance(obj, torch.Tensor):
-            return ("array", tuple(obj.shape), str(obj.dtype).replace("torch.", ""))
-        if obj is None or isinstance(obj, (str, int, float, bool)):
-            return obj
-        if id(obj) in seen:
-            return ("alias", seen[id(obj)])
-        seen[id(obj)] = len(seen)
-        if isinstance(obj, dict):
-            return ("dict", tuple((k, visit(v)) for k, v in sorted(obj.items())))
-        if isinstance(obj, (tuple, list)):
-            return (type(obj).__name__, tuple(visit(v) for v in obj))
-        if hasattr(obj, "__dict__"):
-            return (type(obj).__name__, visit(vars(obj)))
-        raise TypeError(f"cannot describe state field of type {type(obj).__name__}")
+    __slots__ = ("owner", "name")
 
-    return visit(value)
+    def __init__(self, owner: Any, name: str):
+        self.owner, self.name = owner, name
+
+    def get(self) -> Any:
+        o = self.owner
+        if isinstance(o, _INDEXED):
+            return o[int(self.name)]
+        if isinstance(o, _KEYED):
+            return o[self.name]
+        return getattr(o, self.name)
+
+    def put(self, value: Any) -> None:
+        o = self.owner
+        if isinstance(o, tuple):
+            raise TypeError(f"scope step {self.name!r} lives in a tuple, which cannot be "
+                            "assigned; hold swappable children in a list or ModuleList")
+        if isinstance(o, _INDEXED):
+            o[int(self.name)] = value
+        elif isinstance(o, _KEYED):
+            o[self.name] = value
+        else:
+            setattr(o, self.name, value)
+
+
+def _walk(model: Any, path: str) -> _Step:
+    """The last step of ``path`` under ``model``; every step before it resolved."""
+    if not path:
+        raise ValueError("an empty scope path is the model itself; there is no parent "
+                         "to install a wrapper under")
+    names = path.split(".")
+    node = model
+    for depth, name in enumerate(names):
+        step = _Step(node, name)
+        try:
+            child = step.get()
+        except (AttributeError, KeyError, IndexError, ValueError, TypeError) as err:
+            where = ".".join(names[:depth]) or "<model>"
+            raise KeyError(f"cannot resolve scope {path!r}: {type(node).__name__} at {where} "
+                           f"has no child {name!r} ({err})") from None
+        if depth == len(names) - 1:
+            return step
+        node = child
+    raise AssertionError("unreachable")
+
+
+def resolve(model: Any, path: str) -> tuple[Any, str, Any]:
+    """(parent container, last path component, current occupant) of ``path``."""
+    step = _walk(model, path)
+    return step.owner, step.name, step.get()
+
+
+def install(model: Any, path: str, wrapper: nn.Module) -> Any:
+    """Put ``wrapper`` at ``path``; returns the previous occupant."""
+    step = _walk(model, path)
+    previous = step.get()
+    step.put(wrapper)
+    return previous
+
+
+def uninstall(model: Any, path: str, occupant: Any) -> None:
+    """Undo ``install``: ``occupant`` (what install returned) goes back."""
+    _walk(model, path).put(occupant)
+
+
+def _iter_tensors(tree: Any) -> Iterator[torch.Tensor]:
+    if isinstance(tree, torch.Tensor):
+        yield tree
+    elif isinstance(tree, dict):
+        for v in tree.values():
+            yield from _iter_tensors(v)
+    elif isinstance(tree, (list, tuple)):
+        for v in tree:
+            yield from _iter_tensors(v)
+
+
+def flatten_arrays(tree: Any) -> list[torch.Tensor]:
+    """The tensors of a (nested) list / tuple / dict result, depth first in
+    container order; anything else in the tree is skipped."""
+    return list(_iter_tensors(tree))
+
+
+def require_independent_models(first: Any, second: Any) -> None:
+    """Two arms of a comparison may share weight tensors but not modules: a
+    wrapper installed into one arm must leave the other untouched."""
+    if not (isinstance(first, nn.Module) and isinstance(second, nn.Module)):
+        return
+    owned = {id(m): name for name, m in first.named_modules()}
+    shared = [(name or "<root>") for name, m in second.named_modules() if id(m) in owned]
+    if shared:
+        raise ValueError(f"the model builder reused module instance(s) {shared[:3]} across "
+                         "both arms; build fresh modules per arm (weight tensors may be shared)")
 
 
 class ReplayWrapper(nn.Module):
-    """Base for region wrappers: subclasses implement forward as the scope's
-    op stream with the shipped regions spliced in via kernels.try_sized."""
+    """Base class of region wrappers. A subclass's ``forward`` is the scope's
+    op sequence with region kernels called through ``kernels.try_sized`` and
+    the original ops kept for shapes a kernel does not cover. ``_specs`` maps
+    kernel ids to their specs."""
 
     def __init__(self, wrapped: nn.Module, specs: dict | None = None):
         super().__init__()
         self.wrapped = wrapped
-        object.__setattr__(self, "_specs", dict(specs or {}))
+        # a plain attribute, kept out of nn.Module's registries
+        self.__dict__["_specs"] = dict(specs or {})
 
-    def __getattr__(self, name):
+    def __getattr__(self, name: str):
         try:
             return super().__getattr__(name)
         except AttributeError:
-            modules = self.__dict__.get("_modules", {})
-            if "wrapped" not in modules:
+            inner = self.__dict__.get("_modules", {}).get("wrapped")
+            if inner is None:
                 raise
-            return getattr(modules["wrapped"], name)
-
-
-def require_independent_models(first, second) -> None:
-    """Weight tensors may be shared; mutable modules must belong to one arm."""
-    if not isinstance(first, nn.Module) or not isinstance(second, nn.Module):
-        return
-    originals = {id(m) for m in first.modules()}
-    for path, module in second.named_modules():
-        if id(module) in originals:
-            raise ValueError(
-                f"build() reused a model module at {path or '<root>'}; return fresh model "
-                "and layer instances on every call so installing a kernel cannot modify "
-                "the untouched baseline. Weight arrays may be shared.")
-
-
-def _child(obj: object, key: str, full_path: str):
-    try:
-        if isinstance(obj, (list, tuple, nn.ModuleList, nn.Sequential)):
-            return obj[int(key)]
-        if isinstance(obj, nn.ModuleDict):
-            return obj[key]
-        if isinstance(obj, dict):
-            return obj[key]
-        return getattr(obj, key)
-    except (AttributeError, KeyError, IndexError, ValueError, TypeError) as e:
-        raise KeyError(
-            f"cannot resolve scope address {full_path!r}: no child {key!r} on "
-            f"{type(obj).__name__} ({e}); the model tree changed since the trace") from None
-
-
-def resolve(model: object, path: str):
-    """path -> (container, key, child). The empty path (the model itself) has no
-    parent; installing there is the caller's special case."""
-    if path == "":
-        raise ValueError("the root scope has no parent to swap under")
-    parts = path.split(".")
-    obj = model
-    for part in parts[:-1]:
-        obj = _child(obj, part, path)
-    return obj, parts[-1], _child(obj, parts[-1], path)
-
-
-def resolve_value(model: object, path: str):
-    """Resolve a recorded weight or state through modules, dicts and sequences."""
-    obj = model
-    for part in path.split(".") if path else []:
-        obj = _child(obj, part, path)
-    return obj
-
-
-def _assign(parent: object, key: str, value: object) -> None:
-    if isinstance(parent, (list, nn.ModuleList, nn.Sequential)):
-        parent[int(key)] = value
-    elif isinstance(parent, (dict, nn.ModuleDict)):
-        parent[key] = value
-    elif isinstance(parent, tuple):
-        raise TypeError("cannot swap a child living in a tuple; the model must use lists")
-    else:
-        setattr(parent, key, value)
-
-
-def install(model: object, path: str, wrapper: nn.Module) -> object:
-    """Swap ``wrapper`` in at ``path``; returns the previous occupant for rollback."""
-    parent, key, occupant = resolve(model, path)
-    _assign(parent, key, wrapper)
-    return occupant
-
-
-def uninstall(model: object, path: str, occupant: object) -> None:
-    parent, key, _ = resolve(model, path)
-    _assign(parent, key, occupant)
+            return getattr(inner, name)

@@ -347,13 +347,24 @@ def test_require_independent_models():
         swap.require_independent_models(a, b)
 
 
-def test_state_signature_describes_structure_not_data():
-    s1 = {"k": torch.zeros(2, 3), "offset": 4, "both": [1, None]}
-    s2 = {"k": torch.ones(2, 3), "offset": 4, "both": [1, None]}
-    assert swap.state_signature(s1) == swap.state_signature(s2)
-    assert swap.state_signature(s1) != swap.state_signature({**s1, "offset": 5})
-    assert [t.shape for t in swap.flatten_arrays([s1["k"], (torch.zeros(1),)])] == \
-        [(2, 3), (1,)]
+def test_flatten_arrays_walks_nested_results_in_order():
+    a, b, c = torch.zeros(2, 3), torch.zeros(1), torch.zeros(4)
+    got = swap.flatten_arrays([a, (b, 7, None), {"k": c, "n": "x"}])
+    assert [t.shape for t in got] == [(2, 3), (1,), (4,)]
+    assert got[0] is a and got[2] is c
+    assert swap.flatten_arrays(5) == []
+
+
+def test_install_into_dict_and_tuple_children():
+    holder = nn.Module()
+    holder.blocks = nn.ModuleDict({"a": _Block()})
+    old = swap.install(holder, "blocks.a", _Doubler(holder.blocks["a"]))
+    assert isinstance(holder.blocks["a"], _Doubler) and holder.blocks["a"].wrapped is old
+    swap.uninstall(holder, "blocks.a", old)
+    assert holder.blocks["a"] is old
+    frozen = {"t": (_Block(),)}
+    with pytest.raises(TypeError, match="tuple"):
+        swap.install(frozen, "t.0", _Doubler(frozen["t"][0]))
 
 
 def test_apply_installs_an_artifact(tmp_path, stubs):
