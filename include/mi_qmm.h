@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define MI_ABI_VERSION 2  /* 2: mi_argmax takes a workspace */
+#define MI_ABI_VERSION 3  /* 2: mi_argmax takes a workspace; 3: mi_gelu_mlp_f32 */
 
 enum mi_dtype { MI_F32 = 0, MI_F16 = 1, MI_BF16 = 2 };
 
@@ -190,6 +190,24 @@ int mi_shortconv(const void *bx, const void *c, const void *w, const void *state
  * act in {MI_ACT_NONE, MI_ACT_GELU}. */
 int mi_linear_f32(const float *x, const float *w, const float *bias, float *y, int64_t M,
                   int64_t N, int64_t K, int act, void *stream);
+
+/* Config 1's whole tiny MLP as one launch (examples/tiny_mlp.py:5-6: nn.Linear ->
+ * nn.GELU (exact erf) -> nn.Linear, i.e. mx.addmm(b1, x, W1^T), gelu,
+ * mx.addmm(b2, h, W2^T)), fp32:
+ *   y[M, N] = gelu(x[M, K] @ w1[H, K]^T + b1[H]) @ w2[N, H]^T + b2[N].
+ * b1 / b2 may be NULL (zero bias). K and H multiples of 4, K <= 1024; x, w1,
+ * w2 16-byte aligned. The hidden dimension is split over workgroups and the
+ * last workgroup of each 8-row block adds their partial products in a fixed
+ * order, so results are deterministic (a reassociation of the two-linear
+ * stream, within fp32 rounding of it).
+ * workspace: device memory of at least mi_gelu_mlp_f32_workspace_bytes(M, K, H, N)
+ * bytes, 256-byte aligned, whose first bytes (the per-row-block counters) are
+ * zero before its first use; every call leaves them zero again. Calls that
+ * share a workspace must not overlap. */
+int64_t mi_gelu_mlp_f32_workspace_bytes(int64_t M, int64_t K, int64_t H, int64_t N);
+int mi_gelu_mlp_f32(const float *x, const float *w1, const float *b1, const float *w2,
+                    const float *b2, float *y, int64_t M, int64_t K, int64_t H, int64_t N,
+                    void *workspace, int64_t workspace_bytes, void *stream);
 
 /* Greedy sampling (mlx-lm glue; mx.argmax(logits, axis=-1) in mlx-lm's
  * generate loop): out[r] = argmax over x[r, 0:V]; the lowest index wins a

@@ -23,7 +23,7 @@ import torch
 
 PKG = Path(__file__).resolve().parent.parent
 LIB_PATH = Path(os.environ.get("MI_QMM_LIB", PKG / "libmiqmm.so"))
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 MI_F32, MI_F16, MI_BF16 = 0, 1, 2
 MI_OK, MI_ERR_ARG, MI_ERR_UNSUPPORTED, MI_ERR_LAUNCH = 0, 1, 2, 3
@@ -55,10 +55,13 @@ SIGNATURES: dict[str, list] = {
     "mi_swiglu": [_P, _P, _P, _I64, _I, _P],
     "mi_shortconv": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P],
     "mi_linear_f32": [_P, _P, _P, _P, _I64, _I64, _I64, _I, _P],
+    "mi_gelu_mlp_f32_workspace_bytes": [_I64, _I64, _I64, _I64],
+    "mi_gelu_mlp_f32": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
     "mi_argmax_workspace_bytes": [_I64, _I64],
     "mi_argmax": [_P, _P, _I64, _I64, _I, _P, _I64, _P],
 }
-RESTYPES = {"mi_last_error": ctypes.c_char_p, "mi_argmax_workspace_bytes": ctypes.c_int64}
+RESTYPES = {"mi_last_error": ctypes.c_char_p, "mi_argmax_workspace_bytes": ctypes.c_int64,
+            "mi_gelu_mlp_f32_workspace_bytes": ctypes.c_int64}
 
 _lock = threading.Lock()
 _lib = None
@@ -396,6 +399,43 @@ def b_linear_f32(ins, outs, p):
                                int(p.get("act", MI_ACT_NONE)), _stream(x)), "linear_f32")
 
 
+# Workspaces of mi_gelu_mlp_f32 per (device, stream): their ticket counters
+# start at zero (torch.zeros) and every call leaves them zero, so one buffer
+# serves every later call on that stream (calls on one stream never overlap).
+_mlp_workspaces: dict[tuple, torch.Tensor] = {}
+
+
+def _mlp_workspace(device, stream: int, nbytes: int) -> torch.Tensor:
+    key = (device, stream)
+    ws = _mlp_workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 4096), dtype=torch.uint8, device=device)
+        _mlp_workspaces[key] = ws
+    return ws
+
+
+def b_gelu_mlp_f32(ins, outs, p):
+    """inputs (x [M, K], w1 [H, K], b1 [H], w2 [N, H], b2 [N]) -> y [M, N]."""
+    x, w1, b1, w2, b2 = ins
+    (y,) = outs
+    _require_gpu(x)
+    _contig(x, w1, b1, w2, b2, y)
+    if any(t.dtype != torch.float32 for t in (x, w1, b1, w2, b2, y)):
+        raise ValueError("gelu_mlp_f32 takes float32 arrays")
+    if x.dim() != 2 or w1.dim() != 2 or w2.dim() != 2:
+        raise ValueError("gelu_mlp_f32 takes 2-d x, w1, w2")
+    M, K = x.shape
+    H, N = w1.shape[0], w2.shape[0]
+    if (w1.shape[1] != K or w2.shape[1] != H or tuple(b1.shape) != (H,)
+            or tuple(b2.shape) != (N,) or tuple(y.shape) != (M, N)):
+        raise ValueError("gelu_mlp_f32 shapes")
+    stream = _stream(x)
+    nbytes = int(lib().mi_gelu_mlp_f32_workspace_bytes(M, K, H, N))
+    ws = _mlp_workspace(x.device, stream, nbytes)
+    _check(lib().mi_gelu_mlp_f32(_ptr(x), _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2), _ptr(y), M, K,
+                                 H, N, _ptr(ws), ws.numel(), stream), "gelu_mlp_f32")
+
+
 def b_argmax(ins, outs, p):
     (x,) = ins
     (o,) = outs
@@ -430,6 +470,7 @@ BINDINGS: dict[str, Callable] = {
     "mi_swiglu": b_swiglu,
     "mi_shortconv": b_shortconv,
     "mi_linear_f32": b_linear_f32,
+    "mi_gelu_mlp_f32": b_gelu_mlp_f32,
     "mi_argmax": b_argmax,
 }
 

@@ -243,6 +243,15 @@ def linear_f32(x, w, bias=None, gelu: bool = False) -> torch.Tensor:
     return y
 
 
+def gelu_mlp_f32(x, w1, b1, w2, b2) -> torch.Tensor:
+    """Config 1's tiny MLP in one launch: gelu(x W1^T + b1) W2^T + b2 (fp32)."""
+    x = x.contiguous()
+    y = _empty((x.shape[0], w2.shape[0]), x)
+    hip.b_gelu_mlp_f32([x, w1.contiguous(), b1.contiguous(), w2.contiguous(), b2.contiguous()],
+                       [y], {})
+    return y
+
+
 def argmax(x, split: bool = True) -> torch.Tensor:
     """Greedy token: argmax over the last axis (lowest index on ties) as int32.
     split: each row over many workgroups (default) or one workgroup per row;

@@ -16,7 +16,8 @@ wrapper's ``_kernels.try_sized(spec, _ins)`` splice works unchanged:
                     (r036a72bd97248ec8_s0tile_sgfullunroll) -> out
 
 plus the single ops (qmm, dequant, rms_norm, q/k-norm + RoPE, SDPA, swiglu)
-and config 1's tiny MLP as a two-stage region (linear+GELU, linear).
+and config 1's tiny MLP as one launch (``tiny_mlp``; ``tiny_mlp_two_stage`` is the
+same forward as two fp32 linear launches).
 
 Fallback predicates state the shape contract of the entry points (packed
 width and group count consistent with K, K a multiple of the group size),
@@ -200,8 +201,25 @@ def swiglu(kernel_id="swiglu", dtype="bfloat16", ndim=3) -> KernelSpec:
 
 
 def tiny_mlp(kernel_id="tiny_mlp") -> KernelSpec:
-    """Config 1's whole forward as one region of two stages (fp32):
-    tmp0 = gelu(x W1^T + b1); out0 = tmp0 W2^T + b2; inputs (x, W1, b1, W2, b2)."""
+    """Config 1's whole forward as one region and one launch (fp32):
+    out0 = gelu(x W1^T + b1) W2^T + b2 with inputs (x, W1, b1, W2, b2)
+    (examples/tiny_mlp.py:5-6). The hidden dimension is summed in chunks
+    across workgroups in a fixed order, so the region reassociates the
+    two-linear stream (``reassociates``) and is checked at fp32 tolerance."""
+    return KernelSpec(
+        kernel_id=kernel_id, name="mi_gelu_mlp_f32", input_names=tuple(f"in{i}" for i in range(5)),
+        output_names=("out0",), source="mi_gelu_mlp_f32",
+        output_shapes=(("in0.shape[0]", "in3.shape[0]"),), output_dtypes=("float32",),
+        fallback_predicate=("in0.ndim != 2 or in1.shape[1] != in0.shape[1] or "
+                            "in3.shape[1] != in1.shape[0] or in0.shape[1] > 1024 or "
+                            "in0.shape[1] % 4 != 0 or in1.shape[0] % 4 != 0"),
+        reassociates=True)
+
+
+def tiny_mlp_two_stage(kernel_id="tiny_mlp_2") -> KernelSpec:
+    """The same forward as a staged region of two fp32 linear launches
+    (tmp0 = gelu(x W1^T + b1); out0 = tmp0 W2^T + b2), for shapes the one-launch
+    region does not cover."""
     stage0 = KernelSpec(kernel_id=f"{kernel_id}_stage0", name="mi_linear_f32",
                         input_names=("in0", "in1", "in2"), output_names=("out0",),
                         source="mi_linear_f32", output_shapes=(("in0.shape[0]", "in1.shape[0]"),),

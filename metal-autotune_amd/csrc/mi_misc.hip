@@ -143,6 +143,121 @@ __global__ __launch_bounds__(256) void linear_f32_kernel(const float *__restrict
     y[m * N + n] = acc;
 }
 
+// Config 1's whole MLP in one launch: y = gelu(x W1^T + b1) W2^T + b2, fp32.
+// Workgroup (c, rb) takes hidden units [64 c, 64 c + 64) for token rows
+// [8 rb, 8 rb + 8): phase 1 computes those gelu(h) values into LDS (each a
+// sequential fma chain over k, plus b1); phase 2 multiplies them into a
+// partial y tile [8, N] over its 64 hidden units and stores it in the
+// workspace. The last workgroup of a row block to finish (a ticket counter
+// per row block) adds the partials of chunks 0, 1, 2, ... in that fixed order,
+// then b2, and writes y, so the result does not depend on which workgroup
+// finished last. It then resets the counter: the workspace's counters are zero
+// before the first call and after every call.
+constexpr int MLP_HT = 64;      // hidden units per workgroup
+constexpr int MLP_RT = 8;       // token rows per workgroup
+constexpr int MLP_THREADS = 256;
+constexpr int64_t MLP_MAX_K = 1024;  // x rows staged in LDS: 8 x 1024 fp32 = 32 KB
+
+__device__ __forceinline__ float gelu_erf(float v) {
+    return v * (1.0f + erff(v / 1.41421356237f)) / 2.0f;
+}
+
+__global__ __launch_bounds__(MLP_THREADS) void gelu_mlp_f32_kernel(
+    const float *__restrict__ x, const float *__restrict__ w1, const float *__restrict__ b1,
+    const float *__restrict__ w2, const float *__restrict__ b2, float *__restrict__ y,
+    float *__restrict__ part, unsigned *__restrict__ tickets, int64_t M, int64_t K, int64_t H,
+    int64_t N) {
+    extern __shared__ __attribute__((aligned(16))) float mlp_lds[];
+    float *xs = mlp_lds;                       // [MLP_RT][K]
+    float *hs = mlp_lds + MLP_RT * K;          // [MLP_RT][MLP_HT]
+    __shared__ int last;
+    const int t = threadIdx.x;
+    const int64_t c = blockIdx.x, rb = blockIdx.y;
+    const int64_t C = gridDim.x;
+    const int64_t r0 = rb * MLP_RT;
+    const int rows = (int)(M - r0 < MLP_RT ? M - r0 : MLP_RT);
+
+    // stage the row block of x (rows past M read as zero)
+    for (int64_t i = t; i < MLP_RT * K / 4; i += MLP_THREADS) {
+        const int64_t r = (4 * i) / K, k = 4 * i - r * K;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (r < rows) v = *(const float4 *)(x + (r0 + r) * K + k);
+        *(float4 *)(xs + r * K + k) = v;
+    }
+    __syncthreads();
+
+    // phase 1: lane j of wave w computes hidden unit 64 c + j for rows w, w + 4
+    {
+        const int j = t & 63, w = t >> 6;
+        const int64_t hj = c * MLP_HT + j;
+        const int64_t hrow = hj < H ? hj : H - 1;  // clamped, valid row
+        const float *wr = w1 + hrow * K;
+        float a0 = 0.0f, a1 = 0.0f;
+        for (int64_t k = 0; k < K; k += 4) {
+            const float4 wv = *(const float4 *)(wr + k);
+            const float4 xa = *(const float4 *)(xs + w * K + k);
+            const float4 xb = *(const float4 *)(xs + (w + 4) * K + k);
+            a0 = __builtin_fmaf(xa.x, wv.x, a0);
+            a0 = __builtin_fmaf(xa.y, wv.y, a0);
+            a0 = __builtin_fmaf(xa.z, wv.z, a0);
+            a0 = __builtin_fmaf(xa.w, wv.w, a0);
+            a1 = __builtin_fmaf(xb.x, wv.x, a1);
+            a1 = __builtin_fmaf(xb.y, wv.y, a1);
+            a1 = __builtin_fmaf(xb.z, wv.z, a1);
+            a1 = __builtin_fmaf(xb.w, wv.w, a1);
+        }
+        const float bias = b1 ? b1[hrow] : 0.0f;
+        hs[w * MLP_HT + j] = hj < H ? gelu_erf(a0 + bias) : 0.0f;
+        hs[(w + 4) * MLP_HT + j] = hj < H ? gelu_erf(a1 + bias) : 0.0f;
+    }
+    __syncthreads();
+
+    // phase 2: thread t takes output columns n = t, t + 256, ... for all rows
+    const int64_t hbase = c * MLP_HT;
+    const int hn = (int)(H - hbase < MLP_HT ? H - hbase : MLP_HT);  // a multiple of 4
+    float *pc = part + c * (M * N);
+    for (int64_t n = t; n < N; n += MLP_THREADS) {
+        const float *wr = w2 + n * H + hbase;
+        float acc[MLP_RT];
+#pragma unroll
+        for (int r = 0; r < MLP_RT; ++r) acc[r] = 0.0f;
+        for (int hh = 0; hh < hn; hh += 4) {
+            const float4 wv = *(const float4 *)(wr + hh);
+#pragma unroll
+            for (int r = 0; r < MLP_RT; ++r) {
+                const float4 hv = *(const float4 *)(hs + r * MLP_HT + hh);
+                acc[r] = __builtin_fmaf(hv.x, wv.x, acc[r]);
+                acc[r] = __builtin_fmaf(hv.y, wv.y, acc[r]);
+                acc[r] = __builtin_fmaf(hv.z, wv.z, acc[r]);
+                acc[r] = __builtin_fmaf(hv.w, wv.w, acc[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < MLP_RT; ++r)
+            if (r < rows) pc[(r0 + r) * N + n] = acc[r];
+    }
+
+    // phase 3: the last workgroup of this row block reduces the partials
+    __threadfence();  // release: this workgroup's partials before its ticket
+    __syncthreads();
+    if (t == 0) {
+        const unsigned ticket = atomicAdd(&tickets[rb], 1u);
+        last = ticket == (unsigned)(C - 1);
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();  // acquire: every partial of the row block is visible
+    for (int64_t i = t; i < (int64_t)rows * N; i += MLP_THREADS) {
+        const int64_t r = i / N, n = i - r * N;
+        const int64_t o = (r0 + r) * N + n;
+        float s = part[o];
+        for (int64_t cc = 1; cc < C; ++cc) s += part[cc * (M * N) + o];
+        if (b2) s += b2[n];
+        y[o] = s;
+    }
+    if (t == 0) __hip_atomic_store(&tickets[rb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Greedy argmax: one 1024-thread workgroup per row. Each thread keeps the
 // first maximum of the elements it scans (in increasing index order); the
 // (value, index) pairs are then combined with the lowest index winning a tie.
@@ -389,6 +504,44 @@ extern "C" int mi_linear_f32(const float *x, const float *w, const float *bias, 
     const dim3 grid((unsigned)ceil_div(N, 16), (unsigned)ceil_div(M, 16));
     linear_f32_kernel<<<grid, 256, 0, as_stream(stream)>>>(x, w, bias, y, M, N, K, act);
     return launch_status("linear_f32");
+}
+
+// Workspace of mi_gelu_mlp_f32: one ticket counter per row block, then the
+// partial y tiles of every hidden chunk, 256-byte aligned.
+static int64_t mlp_tickets_bytes(int64_t M) { return ceil_div(ceil_div(M, MLP_RT) * 4, 256) * 256; }
+
+extern "C" int64_t mi_gelu_mlp_f32_workspace_bytes(int64_t M, int64_t K, int64_t H, int64_t N) {
+    (void)K;
+    if (M <= 0 || H <= 0 || N <= 0) return 0;
+    return mlp_tickets_bytes(M) + ceil_div(H, MLP_HT) * M * N * (int64_t)sizeof(float);
+}
+
+extern "C" int mi_gelu_mlp_f32(const float *x, const float *w1, const float *b1, const float *w2,
+                               const float *b2, float *y, int64_t M, int64_t K, int64_t H,
+                               int64_t N, void *workspace, int64_t workspace_bytes,
+                               void *stream) {
+    if (M < 0 || K <= 0 || H <= 0 || N < 0) return fail(MI_ERR_ARG, "gelu mlp shape");
+    if (K % 4 || H % 4)
+        return fail(MI_ERR_UNSUPPORTED, "gelu mlp needs K and H multiples of 4 (K=%lld H=%lld)",
+                    (long long)K, (long long)H);
+    if (K > MLP_MAX_K) return fail(MI_ERR_UNSUPPORTED, "gelu mlp K=%lld above %lld", (long long)K,
+                                   (long long)MLP_MAX_K);
+    if (M == 0 || N == 0) return MI_OK;
+    if (!x || !w1 || !w2 || !y || !workspace) return fail(MI_ERR_ARG, "null pointer");
+    if (!aligned(x, 16) || !aligned(w1, 16) || !aligned(w2, 16) || !aligned(workspace, 256))
+        return fail(MI_ERR_ARG, "gelu mlp: x, w1, w2 16-byte aligned, workspace 256-byte aligned");
+    if (ceil_div(M, MLP_RT) > 65535) return fail(MI_ERR_ARG, "gelu mlp: too many rows");
+    const int64_t need = mi_gelu_mlp_f32_workspace_bytes(M, K, H, N);
+    if (workspace_bytes < need)
+        return fail(MI_ERR_ARG, "gelu mlp workspace of %lld bytes, %lld needed",
+                    (long long)workspace_bytes, (long long)need);
+    unsigned *tickets = (unsigned *)workspace;
+    float *part = (float *)((char *)workspace + mlp_tickets_bytes(M));
+    const dim3 grid((unsigned)ceil_div(H, MLP_HT), (unsigned)ceil_div(M, MLP_RT));
+    const size_t lds = (size_t)(MLP_RT * K + MLP_RT * MLP_HT) * sizeof(float);
+    gelu_mlp_f32_kernel<<<grid, MLP_THREADS, lds, as_stream(stream)>>>(x, w1, b1, w2, b2, y, part,
+                                                                       tickets, M, K, H, N);
+    return launch_status("gelu mlp");
 }
 
 extern "C" int64_t mi_argmax_workspace_bytes(int64_t rows, int64_t V) {

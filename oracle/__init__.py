@@ -37,7 +37,14 @@ Pins (all in tests/test_oracle.py):
                       scores give the running mean of v; GQA head mapping
                       h // (H/HK) against per-head repeat; equals a brute
                       force double loop on a tiny case.
-  swiglu, gelu        closed forms (math.erf) on scalars.
+  swiglu, gelu        closed forms (math.erf) on scalars; GELU known values
+                      (Phi(1) = 0.8413447460685429).
+  tiny_mlp            one-hot W1/W2 closed form with nonzero b1 and b2
+                      (y = c * gelu(x[k] + b1[j]) + b2, GELU by math.erf per
+                      scalar); zero W2 -> b2 exactly.
+  norm_rope (layout)  head h of the output == rms_norm then rope of the
+                      contiguous input slice [h*D, (h+1)*D) with positions
+                      along L; permuting input heads permutes output heads.
   shortconv           direct 3-tap sum against a hand-computed case; state
                       carries the last two rows; chunked == whole sequence.
   qwen3_layer         op order of mlx-lm's qwen3 decoder (un-vendored; the

@@ -39,11 +39,30 @@ def test_library_exports_every_declared_symbol(lib):
     assert not missing, f"not exported: {missing}"
 
 
+def header_abi_version() -> int:
+    return int(re.search(r"#define\s+MI_ABI_VERSION\s+(\d+)", HEADER.read_text()).group(1))
+
+
 def test_abi_version_and_error_string(lib):
+    import sys
+    sys.path.insert(0, str(ROOT / "metal-autotune_amd"))
+    from autotuner_runtime import hip
+
     lib.mi_abi_version.restype = ctypes.c_int
     lib.mi_last_error.restype = ctypes.c_char_p
-    assert lib.mi_abi_version() == 2
+    assert lib.mi_abi_version() == header_abi_version() == hip.ABI_VERSION
     assert isinstance(lib.mi_last_error(), bytes)
+
+
+def test_documented_binding_runs_against_the_library():
+    """INTEGRATION.md's reference-side ctypes binding, up to and including its
+    ABI-version assertion, executed against the built library (no device)."""
+    doc = (ROOT / "INTEGRATION.md").read_text()
+    block = re.search(r"```python\n(# autotuner_runtime/hip_backend.py.*?)```", doc, re.S).group(1)
+    setup = block[: block.index("_DT = ")]
+    assert "assert _lib.mi_abi_version() ==" in setup
+    setup = setup.replace("/path/to/metal-autotune_amd/libmiqmm.so", str(LIB))
+    exec(compile(setup, "INTEGRATION.md", "exec"), {})  # raises if the version drifted
 
 
 def test_argmax_workspace_query_needs_no_device(lib):

@@ -3,7 +3,10 @@
 apply() on freshly built models, and validate the artifact in a fresh Python
 process (``python -m autotuner_runtime.artifact validate``), the analog of the
 reference's exported validate.py. Rule: the patched model's logits equal the
-original op streams' bit for bit, both models bitwise repeatable."""
+original op streams' bit for bit, both models bitwise repeatable. The
+installed Qwen3 artifact also has an independent leg: its layers and lm_head
+against the CPU oracle on the same inputs (the reference validates against
+the original MLX ops, an independent path: artifact/validate.py:179-229)."""
 
 from __future__ import annotations
 
@@ -26,6 +29,42 @@ def _fresh_validate(art: Path) -> subprocess.CompletedProcess:
     print(f"\nfresh-process validate {art}", flush=True)
     return subprocess.run([sys.executable, "-m", "autotuner_runtime.artifact", "validate",
                            str(art)], env=env, capture_output=True, text=True, timeout=600)
+
+
+def _oracle_leg_qwen3(patched, run, cfg, n_layers=2):
+    """An independent leg for the installed artifact: each of the first
+    n_layers patched layers (the artifact's wrappers) against the oracle's
+    decoder layer on the same input, and the tied lm_head on the final hidden
+    state against the oracle's, <= 1e-2 max-abs-normalised."""
+    import numpy as np
+
+    import oracle
+    from conftest import to_np
+    from test_models_gpu import _close, _lin, export_layer
+
+    seen = []
+    hooks = [layer.register_forward_hook(lambda m, a, out: seen.append((to_np(a[0]), to_np(out))))
+             for layer in list(patched.model.layers)[:n_layers]]
+    final = []
+    hooks.append(patched.model.norm.register_forward_hook(
+        lambda m, a, out: final.append(to_np(a[0]))))
+    try:
+        logits = to_np(run(patched)[0])
+    finally:
+        for h in hooks:
+            h.remove()
+    assert len(seen) == n_layers and final
+    for (x, y), layer in zip(seen, patched.model.layers):
+        inner = layer.wrapped if hasattr(layer, "wrapped") else layer
+        kc = np.zeros((1, cfg.num_key_value_heads, x.shape[1], cfg.head_dim), np.float32)
+        want = oracle.qwen3_layer(x, export_layer(inner), cfg, 0, kc, np.zeros_like(kc))
+        err = _close(y, want)
+        print(f"artifact layer vs oracle: {err:.3e}")
+    emb = patched.model.embed_tokens
+    hn = oracle.rms_norm(final[-1][:, -1:], to_np(patched.model.norm.weight), cfg.rms_norm_eps,
+                         "bfloat16")
+    want = oracle.qmm_factored(hn, *_lin(emb), cfg.group_size, cfg.bits, "bfloat16")
+    _close(logits.reshape(-1), want.reshape(-1))
 
 
 @pytest.mark.gpu
@@ -53,6 +92,7 @@ def test_qwen3_artifact_round_trip(tmp_path):
     assert torch.equal(run(patched)[0], want) and torch.equal(run(direct)[0], want)
     res, = artifact.validate(art)
     assert res["passed"], res
+    _oracle_leg_qwen3(patched, run, cfg)
     del original, direct, patched
     torch.cuda.empty_cache()
 

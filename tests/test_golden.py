@@ -59,7 +59,7 @@ def _tol(dtype):
 def test_hip_matches_fixture(name):
     import torch
 
-    from autotuner_runtime import ops
+    from autotuner_runtime import kernels, ops, regions
 
     meta, a = make_golden.load(name)
     dt = meta["dtype"]
@@ -95,8 +95,10 @@ def test_hip_matches_fixture(name):
         _close(to_np(out), a["out_out"], _tol(dt))
         assert np.array_equal(to_np(st), a["out_state_out"])  # a copy of the last two rows
     elif op == "tiny_mlp":
-        h = ops.linear_f32(T("x"), T("w1"), T("b1"), gelu=True)
-        got = ops.linear_f32(h, T("w2"), T("b2"))
+        ins = [T("x"), T("w1"), T("b1"), T("w2"), T("b2")]
+        h = ops.linear_f32(ins[0], ins[1], ins[2], gelu=True)
+        _close(to_np(ops.linear_f32(h, ins[3], ins[4])), a["out_y"], 1e-5)   # two launches
+        (got,) = kernels.call(regions.tiny_mlp(), ins, init_value=float("nan"))  # one launch
         _close(to_np(got), a["out_y"], 1e-5)
     elif op == "argmax":
         got = ops.argmax(T("x")).cpu().numpy()

@@ -81,3 +81,54 @@ def test_graph_wrapper_carries_conv_state():
         torch.cuda.synchronize()
         assert torch.equal(got, want) and torch.equal(cg.state, ce.state)
     assert gw.stats["captures"] == 1 and gw.stats["replays"] == 2
+
+
+@pytest.mark.gpu
+def test_graph_wrapper_two_live_conv_states_over_chunks():
+    """Two conv caches, each through two chunks, interleaved: every holder
+    keeps its own state (a replay hands each its own copy), the second chunk
+    of each replays one graph (the carried state is keyed by layout and fed
+    through a static buffer), and both states and outputs equal eager."""
+    from workloads import lfm2
+    from autotuner_runtime.graph import GraphWrapper
+
+    cfg = lfm2.Lfm2Config()
+    model = lfm2.build(cfg, seed=7, num_layers=1, layer_types=("conv",))
+    layer = lfm2.Lfm2ConvRegions(model.model.layers[0], lfm2.layer_specs(cfg))
+    gw = GraphWrapper(layer)
+
+    def chunk(seed):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        return torch.randn((1, 64, cfg.hidden_size), generator=g, device="cuda").to(torch.bfloat16)
+
+    import numpy as np
+
+    import oracle
+    from conftest import to_np
+    from test_lfm2_gpu import _close, export_layer
+
+    W = export_layer(layer)
+    graph_caches = {"a": lfm2.ConvCache(), "b": lfm2.ConvCache()}
+    eager_caches = {"a": lfm2.ConvCache(), "b": lfm2.ConvCache()}
+    order = [("a", 11), ("b", 12), ("a", 13), ("b", 14)]
+    for name, seed in order:
+        x = chunk(seed)
+        state_in = graph_caches[name].state
+        state_in = None if state_in is None else to_np(state_in)
+        got = gw(x, graph_caches[name]).clone()
+        want = layer(x, eager_caches[name])
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (name, seed)
+        # independent leg: a replayed call against the oracle's conv layer
+        o_want, o_state = oracle.lfm2_conv_layer(to_np(x), W, cfg, state_in)
+        _close(to_np(got), o_want)
+        _close(to_np(graph_caches[name].state), o_state)
+        for n in ("a", "b"):
+            gs, es = graph_caches[n].state, eager_caches[n].state
+            assert (gs is None) == (es is None)
+            if gs is not None:
+                assert torch.equal(gs, es), (n, "after", name, seed)
+    ga, gb = graph_caches["a"].state, graph_caches["b"].state
+    assert ga.data_ptr() != gb.data_ptr()
+    assert gw.stats == {"captures": 2, "replays": 2, "eager": 0}

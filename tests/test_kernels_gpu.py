@@ -505,6 +505,54 @@ def test_linear_gelu_f32():
     _close(h, want, "float32", 1e-5)
 
 
+def _mlp_inputs(seed, M, K, H, N, biases=True):
+    r = rng(seed)
+    x = r.normal(0, 1, (M, K)).astype(np.float32)
+    w1 = r.normal(0, 0.02, (H, K)).astype(np.float32)
+    w2 = r.normal(0, 0.02, (N, H)).astype(np.float32)
+    b1 = (r.normal(0, 0.1, H) if biases else np.zeros(H)).astype(np.float32)
+    b2 = (r.normal(0, 0.1, N) if biases else np.zeros(N)).astype(np.float32)
+    return x, w1, b1, w2, b2
+
+
+@pytest.mark.parametrize("M,K,H,N,biases", [
+    (32, 256, 1024, 256, False),   # config 1: b = 0
+    (32, 256, 1024, 256, True),
+    (128, 256, 512, 256, True),    # the reference toy (examples/tiny_mlp.py:5-6)
+    (37, 64, 1000, 72, True),      # ragged rows, a partial last hidden chunk
+])
+def test_tiny_mlp_region_one_launch(M, K, H, N, biases):
+    """Config 1 as one region and one launch (regions.tiny_mlp through
+    kernels.call), NaN-poisoned output, vs oracle.tiny_mlp at fp32 1e-5; three
+    calls are bitwise identical (fixed-order reduction of the hidden chunks,
+    the ticket counters reset by every call)."""
+    from autotuner_runtime import kernels, regions
+
+    host = _mlp_inputs(1410 + M, M, K, H, N, biases)
+    ins = [to_torch(a, "float32") for a in host]
+    spec = regions.tiny_mlp()
+    runs = [kernels.call(spec, ins, init_value=float("nan"))[0] for _ in range(3)]
+    torch.cuda.synchronize()
+    assert not torch.isnan(runs[0]).any()
+    assert all(torch.equal(runs[0], r) for r in runs[1:])
+    want = oracle.tiny_mlp(*[a.astype(np.float64) for a in host])
+    err = _close(runs[0], want, "float32", 1e-5)
+    # the two-launch stream agrees within the same bar
+    h = ops.linear_f32(ins[0], ins[1], ins[2], gelu=True)
+    _close(ops.linear_f32(h, ins[3], ins[4]), want, "float32", 1e-5)
+    print(f"\ntiny mlp {M}x{K}->{H}->{N}: max-abs-normalised error {err:.3e}")
+
+
+def test_tiny_mlp_calls_of_different_sizes_share_the_workspace():
+    """Back-to-back calls of different row counts on one stream (one cached
+    workspace): each equals the oracle, so no ticket or partial leaks from one
+    call into the next."""
+    for i, (M, H) in enumerate(((32, 1024), (9, 256), (32, 1024), (1, 64))):
+        host = _mlp_inputs(1450 + i, M, 256, H, 256)
+        got = ops.gelu_mlp_f32(*[to_torch(a, "float32") for a in host])
+        _close(got, oracle.tiny_mlp(*[a.astype(np.float64) for a in host]), "float32", 1e-5)
+
+
 @pytest.mark.parametrize("split", [True, False])
 @pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
 def test_argmax_lowest_index_on_ties(dtype, split):

@@ -5,8 +5,8 @@ against the CPU oracle composition (oracle.qwen3_layer / qwen3_forward).
 Bars: the region-wrapped layer equals the original op sequence bit for bit
 (the fused epilogues keep every rounding of the unfused ops); against the
 oracle, max-abs-normalised error <= 1e-2 (bf16) per layer output and for the
-final logits, and identical greedy tokens where the oracle's top-2 logit
-margin exceeds the observed logit error (the margin is printed either way).
+final logits, and greedy tokens identical to the oracle's for the config-4
+prefill and decode step (the top-2 margin is printed).
 """
 
 from __future__ import annotations
@@ -104,10 +104,10 @@ def test_qwen3_model_config4_prefill_and_decode():
         input vs the GPU layer output, <= 1e-2 max-abs-normalised;
     (b) the embedding gather bit-exact and the final norm + lm_head on the
         GPU's last hidden state <= 1e-2;
-    (c) free-running: the oracle model from the same token ids; the logit
-        drift is reported (1-ulp bf16 rounding flips compound through 36
-        random-weight layers) and the greedy tokens must agree whenever the
-        oracle's top-2 margin exceeds twice the observed logit error.
+    (c) free-running: the oracle model from the same token ids (its decode
+        step fed the GPU's prefill token); the logit drift (1-ulp bf16
+        rounding flips compound through 36 random-weight layers) stays under
+        0.1 and both greedy tokens equal the oracle's.
     """
     from autotuner_runtime import ops
     from workloads import qwen3
@@ -156,12 +156,12 @@ def test_qwen3_model_config4_prefill_and_decode():
         hn = oracle.rms_norm(hs[-1][:, -1:], fn, cfg.rms_norm_eps, "bfloat16")
         _close(to_np(got), oracle.qmm_factored(hn, *emb, cfg.group_size, cfg.bits, "bfloat16"))
 
-    # (c) free-running oracle
+    # (c) free-running oracle; its decode step takes the GPU's greedy token,
+    # so both decode steps see the same input
     kcs = [np.zeros_like(k) for k in kcs]
     vcs = [np.zeros_like(k) for k in kcs]
     want0 = oracle.qwen3_forward(ids.cpu().numpy(), layers, emb, fn, cfg, 0, kcs, vcs)
-    want1 = oracle.qwen3_forward(np.array([[int(np.argmax(want0))]]), layers, emb, fn, cfg, 128,
-                                 kcs, vcs)
+    want1 = oracle.qwen3_forward(np.array([[tok0]]), layers, emb, fn, cfg, 128, kcs, vcs)
     for got, want, tok, name in ((logits0, want0, tok0, "prefill"), (logits1, want1, tok1, "decode")):
         g = to_np(got).reshape(-1)
         w = want.reshape(-1)
@@ -172,9 +172,13 @@ def test_qwen3_model_config4_prefill_and_decode():
         print(f"config4 {name} free-running: logits max-abs-normalised drift {err:.3e} "
               f"(max abs {abs_err:.3e}), oracle top-2 margin {margin:.3e}, "
               f"greedy token gpu {tok} oracle {int(np.argmax(w))}")
-        assert err < 0.25, f"{name}: logits drift {err:.3e} is beyond rounding compounding"
-        if margin > 2 * abs_err:
-            assert tok == int(np.argmax(w)), f"{name}: greedy token differs"
+        # Free-running drift is 1-ulp bf16 rounding differences compounded
+        # through 36 random-weight layers (each layer is held to 1e-2 in (a));
+        # measured 4.5e-2 (prefill) and 4.7e-2 (decode). The bar is about
+        # twice that: a real defect (a dropped term, a wrong rounding point)
+        # drifts by O(1).
+        assert err < 0.1, f"{name}: logits drift {err:.3e} is beyond rounding compounding"
+        assert tok == int(np.argmax(w)), f"{name}: greedy token differs from the oracle's"
 
 
 def ops_argmax(logits) -> int:

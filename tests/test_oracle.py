@@ -317,6 +317,40 @@ def test_tiny_mlp_bias_path():
     assert (y == np.float32(0.25)).all()
 
 
+def test_tiny_mlp_one_hot_closed_form():
+    """W1 row j picks input k_j, W2 row n picks hidden unit j_n with weight c_n:
+    y[m, n] = c_n * gelu(x[m, k_(j_n)] + b1[j_n]) + b2[n], with GELU from
+    math.erf per scalar. A dropped b1, a GELU after the second linear or a
+    transposed weight fails it."""
+    import math
+
+    r = rng(15)
+    M, K, H, N = 5, 6, 7, 4
+    x = r.normal(0, 1, (M, K))
+    k_of = r.integers(0, K, H)
+    j_of = r.integers(0, H, N)
+    c = r.normal(0, 1, N)
+    w1 = np.zeros((H, K))
+    w1[np.arange(H), k_of] = 1.0
+    w2 = np.zeros((N, H))
+    w2[np.arange(N), j_of] = c
+    b1 = r.normal(0, 1, H)
+    b2 = r.normal(0, 1, N)
+    y = oracle.tiny_mlp(x, w1, b1, w2, b2)
+    for m in range(M):
+        for n in range(N):
+            hval = x[m, k_of[j_of[n]]] + b1[j_of[n]]
+            want = c[n] * hval * (1.0 + math.erf(hval / math.sqrt(2.0))) / 2.0 + b2[n]
+            assert abs(float(y[m, n]) - want) <= 1e-6 * max(1.0, abs(want)), (m, n)
+
+
+def test_gelu_known_values():
+    # exact GELU: x * Phi(x); Phi(1) = 0.8413447460685429
+    g = oracle.gelu(np.array([0.0, 1.0, -1.0, 8.0, -8.0]))
+    np.testing.assert_allclose(g, [0.0, 0.8413447460685429, -0.15865525393145707, 8.0, 0.0],
+                               atol=1e-12)
+
+
 # ---------------------------------------------------------------------- A12
 
 
@@ -478,3 +512,40 @@ def test_lfm2_attn_decode_equals_prefill_last_row():
     oracle.lfm2_attn_layer(seq[:, :5], W, cfg, 0, kc3, vc3)
     wrong = oracle.lfm2_attn_layer(seq[:, 5:], W, cfg, 0, kc3, vc3)
     assert np.abs(wrong - full[:, 5:]).max() / np.abs(full[:, 5:]).max() > 1e-2
+
+
+# ------------------------------------------------------- A6 head layout
+
+
+def test_norm_rope_each_head_is_its_own_slice():
+    """norm_rope(x [B, L, H*D]) at head h equals rms_norm then rope of the
+    contiguous slice x[..., h*D:(h+1)*D] with positions along L: pins the
+    reshape to [B, L, H, D] and the transpose to [B, H, L, D] (a [D, H] split or
+    a missing transpose, which would rotate by head index, fails)."""
+    r = rng(16)
+    B, L, H, D = 2, 5, 3, 8
+    x = oracle.round_to(r.normal(0, 1, (B, L, H * D)), "float32")
+    w = oracle.round_to(r.normal(1, 0.1, D), "float32")
+    out = oracle.norm_rope(x, w, 1e-6, H, D, 1e4, 3, "float32")
+    assert out.shape == (B, H, L, D)
+    for h in range(H):
+        sl = x[:, :, h * D:(h + 1) * D]                       # [B, L, D]
+        want = oracle.rope(oracle.rms_norm(sl, w, 1e-6, "float32"), D, False, 1e4, 1.0, 3,
+                           "float32")
+        np.testing.assert_array_equal(out[:, h], want)
+
+
+def test_norm_rope_permuting_heads_permutes_outputs():
+    r = rng(17)
+    B, L, H, D = 1, 4, 4, 16
+    x = oracle.round_to(r.normal(0, 1, (B, L, H, D)), "bfloat16")
+    w = oracle.round_to(r.normal(1, 0.1, D), "bfloat16")
+    perm = np.array([2, 0, 3, 1])
+    a = oracle.norm_rope(x.reshape(B, L, H * D), w, 1e-6, H, D, 1e6, 0, "bfloat16")
+    b = oracle.norm_rope(x[:, :, perm].reshape(B, L, H * D), w, 1e-6, H, D, 1e6, 0, "bfloat16")
+    np.testing.assert_array_equal(b, a[:, perm])
+    # one head: rms_norm over the row, then rope along the sequence
+    one = oracle.norm_rope(x[:, :, 0], w, 1e-6, 1, D, 1e6, 2, "bfloat16")
+    np.testing.assert_array_equal(
+        one[:, 0], oracle.rope(oracle.rms_norm(x[:, :, 0], w, 1e-6, "bfloat16"), D, False, 1e6,
+                               1.0, 2, "bfloat16"))

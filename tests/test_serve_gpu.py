@@ -31,7 +31,7 @@ def _make_call(cfg):
         gen.manual_seed(1000 + n)
         x = torch.randn((1, n, cfg.hidden_size), generator=gen, device="cuda").to(torch.bfloat16)
         cache = qwen3.KVCache(cfg.num_key_value_heads, cfg.head_dim, 256, "cuda")
-        return (mod(x, cache), cache.keys, cache.values)
+        return (mod(x, cache), cache.keys, cache.values, x)
     return call
 
 
@@ -85,6 +85,16 @@ def test_ranges_gate_the_kernels(monkeypatch):
         ref = call(layer, n)
         torch.cuda.synchronize()
         assert all(torch.equal(a, b) for a, b in zip(got, ref))
+    # an independent leg at a served size: the layer against the oracle's
+    import numpy as np
+
+    import oracle
+    from conftest import to_np
+    from test_models_gpu import _close, export_layer
+
+    kc = np.zeros((1, cfg.num_key_value_heads, 100, cfg.head_dim), np.float32)
+    want = oracle.qwen3_layer(to_np(got[3]), export_layer(layer), cfg, 0, kc, np.zeros_like(kc))
+    print(f"\nserved size 100 vs oracle: {_close(to_np(got[0]), want):.3e}")
 
 
 @pytest.mark.gpu
