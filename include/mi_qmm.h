@@ -36,7 +36,8 @@
 extern "C" {
 #endif
 
-#define MI_ABI_VERSION 3  /* 2: mi_argmax takes a workspace; 3: mi_gelu_mlp_f32 */
+#define MI_ABI_VERSION 4  /* 2: mi_argmax takes a workspace; 3: mi_gelu_mlp_f32;
+                             4: mi_argmax_noalloc */
 
 enum mi_dtype { MI_F32 = 0, MI_F16 = 1, MI_BF16 = 2 };
 
@@ -220,6 +221,18 @@ int mi_gelu_mlp_f32(const float *x, const float *w1, const float *b1, const floa
 int64_t mi_argmax_workspace_bytes(int64_t rows, int64_t V);
 int mi_argmax(const void *x, int32_t *out, int64_t rows, int64_t V, int dtype, void *workspace,
               int64_t workspace_bytes, void *stream);
+
+/* No counterpart in the reference. mi_argmax for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc): no workspace argument and no allocation. The
+ * per-span partials live in a fixed device array of the library, 8192
+ * entries (64 KiB) per GPU, looked up on the first call on a device and held
+ * until the process ends. rows x spans must fit it (spans = ceil(V * size /
+ * 8192 bytes) for 16-byte-aligned rows, e.g. at most 215 rows of
+ * V = 151936 bf16), else MI_ERR_ARG. Same result as mi_argmax. Calls that
+ * overlap on one GPU race on that array. */
+int mi_argmax_noalloc(const void *x, int32_t *out, int64_t rows, int64_t V, int dtype,
+                      void *stream);
 
 #ifdef __cplusplus
 }

@@ -23,7 +23,7 @@ import torch
 
 PKG = Path(__file__).resolve().parent.parent
 LIB_PATH = Path(os.environ.get("MI_QMM_LIB", PKG / "libmiqmm.so"))
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 MI_F32, MI_F16, MI_BF16 = 0, 1, 2
 MI_OK, MI_ERR_ARG, MI_ERR_UNSUPPORTED, MI_ERR_LAUNCH = 0, 1, 2, 3
@@ -59,6 +59,7 @@ SIGNATURES: dict[str, list] = {
     "mi_gelu_mlp_f32": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
     "mi_argmax_workspace_bytes": [_I64, _I64],
     "mi_argmax": [_P, _P, _I64, _I64, _I, _P, _I64, _P],
+    "mi_argmax_noalloc": [_P, _P, _I64, _I64, _I, _P],
 }
 RESTYPES = {"mi_last_error": ctypes.c_char_p, "mi_argmax_workspace_bytes": ctypes.c_int64,
             "mi_gelu_mlp_f32_workspace_bytes": ctypes.c_int64}

@@ -4,6 +4,8 @@
 // allows, one thread per 8 values.
 #include <math.h>
 
+#include <mutex>
+
 #include "mi_common.h"
 
 namespace mi {
@@ -435,6 +437,44 @@ int64_t am_spans(int64_t V, int esize, bool vec) {
 }  // namespace
 }  // namespace mi
 
+// Scratch of mi_argmax_noalloc: the per-span partials of the split argmax,
+// AM_NOALLOC_PARTS entries (64 KiB) in a file-scope device array, one copy per
+// GPU, held until the process ends. Host code never passes the array's name
+// to a kernel (on the host it is only a stand-in symbol): the first call on a
+// device looks up that device's copy with hipGetSymbolAddress and keeps the
+// pointer. Calls on one GPU share the array, so calls that overlap on one GPU
+// race; every call overwrites the partials it reads, so nothing has to start
+// at zero.
+#define AM_NOALLOC_PARTS 8192
+static __device__ __align__(256) mi::AmPart scratch[AM_NOALLOC_PARTS];
+
+namespace {
+constexpr int AM_MAX_DEVICES = 64;
+std::mutex am_scratch_lock;
+mi::AmPart *am_scratch_ptr[AM_MAX_DEVICES];
+
+// This device's copy of `scratch` (found once per device), or NULL after
+// recording an error.
+mi::AmPart *am_scratch(int dev) {
+    if (dev < 0 || dev >= AM_MAX_DEVICES) {
+        mi::fail(MI_ERR_ARG, "argmax_noalloc: device %d beyond %d", dev, AM_MAX_DEVICES);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> guard(am_scratch_lock);
+    if (am_scratch_ptr[dev] == nullptr) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            mi::fail(MI_ERR_LAUNCH, "argmax_noalloc: hipGetSymbolAddress on device %d: %s", dev,
+                     hipGetErrorString(e));
+            return nullptr;
+        }
+        am_scratch_ptr[dev] = (mi::AmPart *)p;
+    }
+    return am_scratch_ptr[dev];
+}
+}  // namespace
+
 using namespace mi;
 
 extern "C" int mi_swiglu(const void *g, const void *u, void *y, int64_t n, int dtype,
@@ -591,4 +631,45 @@ extern "C" int mi_argmax(const void *x, int32_t *out, int64_t rows, int64_t V, i
         MI_AM(float);
 #undef MI_AM
     return launch_status("argmax");
+}
+
+extern "C" int mi_argmax_noalloc(const void *x, int32_t *out, int64_t rows, int64_t V, int dtype,
+                                 void *stream) {
+    if (!valid_dtype(dtype)) return fail(MI_ERR_UNSUPPORTED, "dtype code %d", dtype);
+    if (rows < 0 || V <= 0) return fail(MI_ERR_ARG, "argmax shape");
+    if (V > INT32_MAX) return fail(MI_ERR_ARG, "argmax row of %lld values exceeds int32", (long long)V);
+    if (rows == 0) return MI_OK;
+    if (!x || !out) return fail(MI_ERR_ARG, "null pointer");
+    const int esize = dtype == MI_F32 ? 4 : 2;
+    const bool vec = aligned(x, 16) && (V * esize) % 16 == 0;
+    const int64_t G = am_spans(V, esize, vec);
+    if (rows > 65535 || rows * G > AM_NOALLOC_PARTS)
+        return fail(MI_ERR_ARG,
+                    "argmax_noalloc: %lld rows x %lld spans of partials exceed its fixed scratch "
+                    "of %d (use mi_argmax with a workspace)",
+                    (long long)rows, (long long)G, AM_NOALLOC_PARTS);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(MI_ERR_LAUNCH, "argmax_noalloc: no device");
+    AmPart *part = am_scratch(dev);
+    if (!part) return MI_ERR_LAUNCH;
+    hipStream_t st = as_stream(stream);
+    const dim3 grid((unsigned)G, (unsigned)rows);
+#define MI_AMN(TT)                                                                              \
+    do {                                                                                        \
+        if (vec)                                                                                \
+            argmax_part_kernel<TT, true><<<grid, AM_SPLIT_THREADS, 0, st>>>((const TT *)x, part, \
+                                                                           V);                 \
+        else                                                                                    \
+            argmax_part_kernel<TT, false><<<grid, AM_SPLIT_THREADS, 0, st>>>((const TT *)x,     \
+                                                                            part, V);          \
+        argmax_merge_kernel<<<(unsigned)rows, 64, 0, st>>>(part, (int)G, out);                 \
+    } while (0)
+    if (dtype == MI_BF16)
+        MI_AMN(bf16);
+    else if (dtype == MI_F16)
+        MI_AMN(f16);
+    else
+        MI_AMN(float);
+#undef MI_AMN
+    return launch_status("argmax_noalloc");
 }
