@@ -179,26 +179,32 @@ def cpu_baseline(model, ids, torch):
     x = oracle.round_to(r.normal(0, 1, (1, PROMPT, cfg.hidden_size)), "bfloat16")
     kc = np.zeros((1, cfg.num_key_value_heads, PROMPT, cfg.head_dim), np.float32)
     vc = np.zeros_like(kc)
-    # repeat the layer until ~10 s of CPU work (at most 36 layers' worth)
-    reps, t0 = 0, time.perf_counter()
-    while reps < cfg.num_hidden_layers and (reps == 0 or time.perf_counter() - t0 < 10.0):
-        oracle.qwen3_layer(x, W, cfg, 0, kc, vc)
-        reps += 1
-    t_layer = (time.perf_counter() - t0) / reps
-    t0 = time.perf_counter()
-    oracle.qmm_factored(x[:, -1:], *E, cfg.group_size, cfg.bits, "bfloat16")
-    t_head = time.perf_counter() - t0
-    total = cfg.num_hidden_layers * t_layer + t_head
     cores = len(os.sched_getaffinity(0))
     omp = os.environ.get("OMP_NUM_THREADS")
     if omp and omp.isdigit():
         cores = min(cores, int(omp))
+    gs, bits = cfg.group_size, cfg.bits
+
+    def proj(a, lin):
+        # the reference's restated qmm (per-group factored sum, fp32), C/OpenMP
+        return oracle.qmm_factored(a, *lin, gs, bits, "bfloat16", nthreads=cores)
+
+    # repeat the layer until ~10 s of CPU work (at most 36 layers' worth)
+    reps, t0 = 0, time.perf_counter()
+    while reps < cfg.num_hidden_layers and (reps == 0 or time.perf_counter() - t0 < 10.0):
+        oracle.qwen3_layer(x, W, cfg, 0, kc, vc, qmm=proj)
+        reps += 1
+    t_layer = (time.perf_counter() - t0) / reps
+    t0 = time.perf_counter()
+    oracle.qmm_factored(x[:, -1:], *E, gs, bits, "bfloat16", nthreads=cores)
+    t_head = time.perf_counter() - t0
+    total = cfg.num_hidden_layers * t_layer + t_head
     return {"value": round(PROMPT / total, 2), "unit": "tok/s", "cores": cores, "kind": "port",
             "sample": f"oracle: decoder layer 0 at L={PROMPT}, run {reps}x ({t_layer:.2f} s "
                       f"each) + lm_head for 1 token ({t_head:.2f} s), scaled to the "
-                      f"{cfg.num_hidden_layers}-layer model; numpy float64 BLAS for M=128 "
-                      "projections, C/OpenMP factored qmm for the lm_head; MLX CPU backend "
-                      "unavailable (mlx not installed, no network)"}
+                      f"{cfg.num_hidden_layers}-layer model; every projection through the C/OpenMP "
+                      f"restatement of the factored qmm on {cores} threads, norms/RoPE/attention "
+                      "in numpy; MLX CPU backend unavailable (mlx not installed, no network)"}
 
 
 def lfm2_config5(torch, ops, reps: int = 10) -> dict:

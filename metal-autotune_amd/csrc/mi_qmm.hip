@@ -500,18 +500,14 @@ template <> struct Mfma<f16> {
 };
 
 // A: 32-row weight tiles per wave (one per part when P > 1); C: 32-token
-// tiles per wave; WK: waves per workgroup; WF: waves that share one x stage
-// and each own a different 32 * A-feature tile. The workgroup's waves form
-// wk = (waves / WF) K-groups, each owning a 1/wk slice of K.
+// tiles per wave; WK: waves per workgroup, each owning a 1/wk slice of K.
 //
-// Everything a stage needs reaches the waves through LDS by direct-to-LDS DMA
-// (buffer_load ... lds), into a ring of PIPE stage slots per K-group:
+// Everything a stage needs reaches a wave through LDS by direct-to-LDS DMA
+// (buffer_load ... lds), into the wave's one stage slot:
 //  * the x tile of the stage, 8 token rows x 128 bytes per instruction, so
 //    every x cache line is fetched once (loading x fragments straight into
 //    registers makes each lane read a different token row, and with four
-//    waves the per-step working set overflows the 32 KB L1). The WF waves of
-//    a K-group issue 1/WF of those instructions each and meet at a barrier
-//    before reading the tile. The 16-byte
+//    waves the per-step working set overflows the 32 KB L1). The 16-byte
 //    chunks of a row are XOR-swizzled by (row >> 1) & 7 so a 16-lane
 //    ds_read_b128 group covers 16 distinct bank groups;
 //  * each lane's 16-byte weight chunk, per part and super-step (lane l's
@@ -528,9 +524,7 @@ template <> struct Mfma<f16> {
 constexpr int XK = 64;  // k values per x stage (128 bytes of a token row)
 constexpr int LDS_PER_CU = 160 * 1024;
 
-constexpr int MAX_PIPE = 8;  // ring slots per K-group at most
-
-template <typename T, int BITS, int A, int C, int WK, int PIPE, int WF = 1>
+template <typename T, int BITS, int A, int C, int WK>
 struct MfmaShape {
     static constexpr int VPW = 32 / BITS;  // values per word
     static constexpr int VPC = 4 * VPW;    // values per 16-byte weight chunk (per lane half)
@@ -538,44 +532,33 @@ struct MfmaShape {
     static constexpr int SS = 2 * VPC;     // k per super-step
     static constexpr int SPS = XK / SS;    // super-steps per x stage
     static constexpr int ROWS = 32 * C;    // token rows per stage
-    static constexpr int KG = WK / WF;     // K-groups at most
-    // Several weight tiles per wave (A > 1) with one wave per x stage: their
-    // chunks are prefetched one stage ahead into registers instead of the
-    // ring, which keeps the ring small enough for two workgroups per CU.
-    static constexpr bool WREG = A > 1 && WF == 1;
+    static constexpr int KG = WK;          // K-groups (one wave each)
+    // Several weight tiles per wave (A > 1): their chunks are prefetched one
+    // stage ahead into registers instead of the slot, which keeps the slots
+    // small enough for two workgroups per CU.
+    static constexpr bool WREG = A > 1;
     static constexpr int XST = ROWS * 128;                           // x tile bytes per stage
     static constexpr int WAVE = WREG ? 0 : A * SPS * 1024;           // a wave's weight chunks
-    static constexpr int STAGE = XST + WF * WAVE;                    // one ring slot
-    static constexpr int XBYTES = KG * PIPE * STAGE;                 // stage rings
-    // PIPE == 1: one slot per wave; a stage reads its slot into registers,
-    // then the next stage's DMAs refill it (LEAD: stages issued ahead)
-    static constexpr bool SINGLE = PIPE == 1;
-    static constexpr int LEAD = SINGLE ? 1 : PIPE - 1;
+    static constexpr int STAGE = XST + WAVE;                         // one wave's slot
+    static constexpr int XBYTES = KG * STAGE;                        // the workgroup's slots
     // K-split reduction: the partial tiles of K-groups 1..KG-1 pass through
-    // the ring's LDS, RSLOTS at a time
-    static constexpr int PB = WF * A * C * 16 * 64 * 4;              // one K-group's partials
+    // the slots' LDS, RSLOTS at a time
+    static constexpr int PB = A * C * 16 * 64 * 4;                   // one K-group's partials
     static constexpr int RSLOTS = KG <= 1 ? 1 : (XBYTES / PB >= KG - 1 ? KG - 1
                                                  : (XBYTES / PB > 0 ? XBYTES / PB : 1));
     static constexpr int RBYTES = RSLOTS * PB;
     static constexpr int LDS = XBYTES > RBYTES ? XBYTES : RBYTES;
-    // DMA instructions a lane issues per stage: its share of x, and weights
-    static constexpr int XOPS = ROWS / 8 / WF;
+    // DMA instructions a lane issues per stage: its x rows, and weights
+    static constexpr int XOPS = ROWS / 8;
     static constexpr int OPS = XOPS + (WREG ? 0 : A * SPS);
-    // vmcnt at the top of a stage: the loads of the LEAD - 1 stages issued
-    // after it may still be in flight (vmcnt decrements in issue order)
-    static constexpr int VMCNT = (LEAD - 1) * OPS;
-    // vmcnt once the ring prologue (LEAD stages of DMAs, plus the first
-    // stage's register weights) is issued: only the scale/bias table before it
-    // has landed
-    static constexpr int TABLE_VMCNT = LEAD * OPS + (WREG ? A * SPS : 0);
-    // the stage loop is unrolled so ring slots and the two register weight
-    // sets are named statically
-    static constexpr int UNROLL = PIPE < 2 ? 2 : PIPE;
-    static_assert(WK % WF == 0 && (ROWS / 8) % WF == 0, "x instructions split evenly");
-    static_assert(PIPE >= 1 && PIPE <= MAX_PIPE && TABLE_VMCNT < 64, "vmcnt is a 6-bit count");
-    static_assert(!WREG || PIPE <= 2, "register-prefetched weights run one stage ahead");
-    static_assert(!SINGLE || WF == 1, "a shared single slot would need a barrier before its refill");
-    static_assert(LDS <= LDS_PER_CU, "stage rings exceed the LDS of a CU");
+    // vmcnt once the prologue (the first stage's DMAs, plus its register
+    // weights) is issued: only the scale/bias table before it has landed
+    static constexpr int TABLE_VMCNT = OPS + (WREG ? A * SPS : 0);
+    // the stage loop is unrolled twice so the two register weight sets are
+    // named statically
+    static constexpr int UNROLL = 2;
+    static_assert(TABLE_VMCNT < 64, "vmcnt is a 6-bit count");
+    static_assert(LDS <= LDS_PER_CU, "stage slots exceed the LDS of a CU");
 };
 
 // Scale/bias table of one wave: for each of its A weight tiles, the scales
@@ -605,24 +588,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, 
                                              0x00020000);
 }
 
-// Ring slots per wave (MI_QMM_MAX_PIPE, a build-time tuning knob). Measured
-// on MI355X at the Qwen3 prefill shapes (M = 128), one slot wins: it halves
-// the ring, so three workgroups share a CU (three waves per SIMD, which
-// overlap one wave's dequant VALU with the others' MFMAs and loads), where
-// two slots allowed two workgroups and three slots one. Dual 38.0 -> 32.9 us,
-// q/k/v 15.0 -> 13.8, o_proj 12.1 -> 11.5, bit for bit the same results.
-// Above one, the deepest ring whose four waves' slots fit the LDS of a CU.
-#ifndef MI_QMM_MAX_PIPE
-#define MI_QMM_MAX_PIPE 1
-#endif
-template <typename T, int BITS, int A, int C> constexpr int mfma_pipe() {
-    typedef MfmaShape<T, BITS, A, C, 4, 2, 1> Sh2;
-    if constexpr (MI_QMM_MAX_PIPE <= 1) return 1;
-    if constexpr (Sh2::WREG) return 2;
-    constexpr int slot = Sh2::STAGE;
-    constexpr int fit = 4 * 4 * slot <= LDS_PER_CU ? 4 : (4 * 3 * slot <= LDS_PER_CU ? 3 : 2);
-    return fit < MI_QMM_MAX_PIPE ? fit : MI_QMM_MAX_PIPE;
-}
+// One stage slot per wave. Measured on MI355X at the Qwen3 prefill shapes
+// (M = 128), it beats rings of two to eight slots: the small footprint lets
+// three workgroups share a CU (three waves per SIMD, which overlap one wave's
+// dequant VALU with the others' MFMAs and loads), where two slots allowed two
+// workgroups and three slots one. Dual 38.0 -> 32.9 us, q/k/v 15.0 -> 13.8,
+// o_proj 12.1 -> 11.5, bit for bit the same results. (A balanced grid of one
+// workgroup per CU gains nothing from deeper rings either: 25.9 us with one
+// slot, 27.7 us with two or three, dual at N = 8192.)
 
 // s_waitcnt with vmcnt = N and no wait on the other counters (gfx9 encoding:
 // vmcnt[3:0] at bits 3:0 and vmcnt[5:4] at bits 15:14, expcnt 7, lgkmcnt 15).
@@ -636,37 +609,26 @@ __device__ __forceinline__ void wait_lgkmcnt0() {
     __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
 }
 
-// Workgroup barrier with no memory fence: the waves have already waited for
-// their own DMAs into the stage (vmcnt), and LDS is one store per CU, so the
-// barrier alone makes the whole stage visible. (__syncthreads' fences would
-// also wait for the DMAs still filling the later slots.) The empty asm
-// statements keep the compiler from moving LDS accesses across it.
-__device__ __forceinline__ void stage_barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
-// Waves per SIMD the register allocation must allow: the single-slot ring
-// exists so three workgroups of four waves share a CU (at most 168 registers
-// a lane), which tiles of up to four 32x32 accumulators fit without spilling;
+// Waves per SIMD the register allocation must allow: the single slot exists
+// so three workgroups of four waves share a CU (at most 168 registers a
+// lane), which tiles of up to four 32x32 accumulators fit without spilling;
 // larger tiles, and 128-token tiles (whose slot alone leaves room for two
 // workgroups), ask for two (256 registers).
-template <int PIPE, int A, int C> constexpr int mfma_waves_per_eu() {
-    return PIPE == 1 ? (A * C <= 4 && C <= 2 ? 3 : 2) : 1;
+template <int A, int C> constexpr int mfma_waves_per_eu() {
+    return A * C <= 4 && C <= 2 ? 3 : 2;
 }
 
 // One workgroup's tile: tokens [m_blk, m_blk + 32 * C) of the output features
-// starting at n_blk (32 * TN * WF of them, per part). lds is the workgroup's
-// static LDS, at least MfmaShape::LDS bytes; the scale/bias tables live in
-// the dynamic LDS.
-template <typename T, int BITS, int A, int C, int WK, int PIPE, int EPI, int WF>
+// starting at n_blk (32 * TN of them, per part). lds is the workgroup's static
+// LDS, at least MfmaShape::LDS bytes; the scale/bias tables live in the
+// dynamic LDS.
+template <typename T, int BITS, int A, int C, int WK, int EPI>
 __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64_t n_blk,
                                               int64_t m_blk) {
     // The body uses gfx950 buffer resources, which the host target cannot
     // type; the host pass needs only the kernels' launch stubs.
 #if defined(__HIP_DEVICE_COMPILE__)
-    typedef MfmaShape<T, BITS, A, C, WK, PIPE, WF> Sh;
+    typedef MfmaShape<T, BITS, A, C, WK> Sh;
     constexpr int P = epi_parts(EPI);
     static_assert(P == 1 || A == P, "multi-part epilogues use one tile per part");
     constexpr int TN = (P == 1) ? A : 1;  // 32-wide output tiles per wave
@@ -674,22 +636,20 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
     typedef typename Vec<T>::x8 V8;
 
     const int lane = threadIdx.x & 63;
-    // the wave indices are uniform per wave: in scalar registers, the x stage
+    // the wave index is uniform per wave: in a scalar register, the x stage
     // base addresses and the DMA's LDS destinations (M0) need no VALU work.
-    // Wave w owns feature tile fw = w % WF of the workgroup's WF tiles, in
-    // K-group kw = w / WF.
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int fw = wv % WF, kw = wv / WF;
+    // Wave kw owns the K slice kw of the workgroup's wk.
+    const int kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = lane >> 5, r = lane & 31;
     const int64_t K = p.K, G = K / p.gs;
-    int64_t n_wave = n_blk + fw * (32 * TN);
+    int64_t n_wave = n_blk;
     const Bound bd = bind<EPI>(p, n_wave);
     const int wk = p.wk;
     const int Kw = (int)(K / wk);
     const int kbeg = kw * Kw;
     const int nst = Kw / XK;
-    char *xbuf = lds + kw * PIPE * Sh::STAGE;
-    const int wslot = Sh::XST + fw * Sh::WAVE;  // this wave's weights within a slot
+    char *xbuf = lds + kw * Sh::STAGE;
+    const int wslot = Sh::XST;  // this wave's weights within its slot
 
     // Rows past N (or tokens past M) read a clamped, valid row instead of
     // branching around the load: their accumulators only feed outputs the
@@ -718,7 +678,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
     const int pitch = p.sbp;
     const SbtLayout tl = sbt_layout(Kw, p.gs);
     extern __shared__ __attribute__((aligned(16))) char lds_dyn[];
-    const char *sbt = lds_dyn + wv * (A * 2 * tl.array_bytes);
+    const char *sbt = lds_dyn + kw * (A * 2 * tl.array_bytes);
     const int gbase = (kbeg >> gshift) & ~1;
     typedef __attribute__((address_space(3))) void *lds_ptr;
     for (int i = 0; i < tl.ninst; ++i) {
@@ -741,7 +701,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
     const int sbrow = (r * pitch + hg - gbase) * 2;
     // x DMA: instruction i writes stage rows 8i..8i+7; lane l fills row
     // 8i + l/8 at swizzled position l%8, i.e. it loads chunk (l%8) ^ swz(row).
-    // Wave fw issues instructions i = WF * j + fw. Tokens past M point past
+    // Tokens past M point past
     // the end of x's buffer resource: the load returns zeros without a memory
     // access, and every lane still issues the same instructions (the end
     // offset plus a stage offset stays below 2^32 since M * K * size < 2^31).
@@ -750,7 +710,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
     uint32_t xoff[Sh::XOPS];
 #pragma unroll
     for (int j = 0; j < Sh::XOPS; ++j) {
-        const int row = 8 * (WF * j + fw) + (lane >> 3);
+        const int row = 8 * j + (lane >> 3);
         const int chunk = (lane & 7) ^ ((row >> 1) & 7);
         xoff[j] = m_blk + row < p.M
                       ? (uint32_t)(((m_blk + row) * K + 8 * chunk) * (int64_t)sizeof(T))
@@ -761,9 +721,8 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
         const uint32_t xs = (uint32_t)k0 * sizeof(T);
 #pragma unroll
         for (int j = 0; j < Sh::XOPS; ++j)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(slot + (WF * j + fw) * 1024), 16,
-                                                     xoff[j],
-                                                     xs, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(slot + j * 1024), 16, xoff[j], xs,
+                                                     0, 0);
         if constexpr (Sh::WREG) return;
 #pragma unroll
         for (int u = 0; u < SPS; ++u) {
@@ -804,34 +763,24 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[a][c][i] = 0.0f;
 
-    // Pipeline, PIPE stages deep: while stage st computes, the DMAs of stage
-    // st + PIPE - 1 fill ring slot (st + PIPE - 1) % PIPE, which was last read
-    // by stage st - 1 (its ds_reads completed before its MFMAs; with WF > 1
-    // the barrier at the top of stage st also waits for the other waves to
-    // finish stage st - 1). PIPE == 1: one slot; stage st reads it into
-    // registers, waits for those reads, then refills it with stage st + 1.
-    // Every stage issues exactly OPS DMAs -- past the last stage they re-read
-    // stage nst - 1, in bounds, into slots no later stage reads -- so at the
-    // top of stage st at most the loads of the LEAD - 1 stages after it are in
-    // flight: vmcnt(VMCNT). The stage loop is unrolled (UNROLL) so each slot
-    // and register weight set is named statically.
+    // Pipeline: stage st reads the wave's slot into registers, waits for those
+    // reads, then refills the slot with stage st + 1 and computes while those
+    // DMAs fly. Every stage issues exactly OPS DMAs -- past the last stage
+    // they re-read stage nst - 1, in bounds, into the slot no later stage
+    // reads -- so at the top of a stage nothing else is in flight: vmcnt(0).
+    // The stage loop is unrolled twice so the two register weight sets are
+    // named statically.
     //
-    // The slots (and the scale/bias table) are passed as separate __restrict__
+    // The slot and the scale/bias table are passed as separate __restrict__
     // arguments of the inlined main loop: the resulting alias scopes let the
-    // compiler's wait-count pass see that a stage's ds_reads cannot touch the
-    // slots the DMAs in flight are filling, so it adds no vmcnt(0) of its own
-    // before them. The table's DMAs precede the ring prologue's, so the wait
-    // at the top of stage 0 retires them.
+    // compiler's wait-count pass see that a stage's table reads cannot touch
+    // the slot the DMAs in flight are filling, so it adds no vmcnt(0) of its
+    // own before them. The table's DMAs precede the prologue's, so the wait at
+    // the top of stage 0 retires them.
     const int swz = (r >> 1) & 7;
     const int tab = tl.array_bytes;
-    auto mainloop = [&](char *__restrict__ b0, char *__restrict__ b1, char *__restrict__ b2,
-                        char *__restrict__ b3, char *__restrict__ b4, char *__restrict__ b5,
-                        char *__restrict__ b6, char *__restrict__ b7,
-                        const char *__restrict__ tb) __attribute__((always_inline)) {
-    auto ring = [&](int j) -> char * {
-        return j == 0 ? b0 : j == 1 ? b1 : j == 2 ? b2 : j == 3 ? b3 : j == 4 ? b4 : j == 5 ? b5
-               : j == 6 ? b6 : b7;
-    };
+    auto mainloop = [&](char *__restrict__ slot, const char *__restrict__ tb)
+                        __attribute__((always_inline)) {
     const int last = nst > 0 ? nst - 1 : 0;
     // Scales and biases of a stage are read from the table one stage ahead,
     // so a stage's first dequant waits only for its weight chunk, not for the
@@ -847,10 +796,9 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
                 bq[a][u] = *(const uint16_t *)(sb + tab);
             }
     };
-#pragma unroll
-    for (int j = 0; j < Sh::LEAD; ++j) issue(j < last ? j : last, ring(j % PIPE));
+    issue(0, slot);
     if constexpr (Sh::WREG) load_w(0, wreg[0]);
-    // the table's DMAs were issued before the ring prologue's
+    // the table's DMAs were issued before the prologue's
     wait_vmcnt<Sh::TABLE_VMCNT>();
     load_sb(0);
     for (int st0 = 0; st0 < nst; st0 += Sh::UNROLL) {
@@ -858,9 +806,8 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
         for (int j = 0; j < Sh::UNROLL; ++j) {
             const int st = st0 + j;
             if (st >= nst) break;  // workgroup-uniform
-            wait_vmcnt<Sh::VMCNT>();
-            if constexpr (WF > 1) stage_barrier();
-            const char *cur = ring(j % PIPE);
+            wait_vmcnt<0>();
+            const char *cur = slot;
             // the weight chunk first: the first dequant needs it, while the
             // MFMAs that consume the x fragments come after that dequant
             uint4 wq[A][SPS];
@@ -911,15 +858,11 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
                     launder(opa[k]);  // computed here, not sunk to its MFMA
                 }
             }
-            const int nx = st + Sh::LEAD < last ? st + Sh::LEAD : last;
-            if constexpr (Sh::SINGLE) {
-                // the slot's reads have returned before its refill is issued
-                __builtin_amdgcn_sched_barrier(0);
-                wait_lgkmcnt0();
-                issue(nx, ring(0));
-            } else {
-                issue(nx, ring((j + PIPE - 1) % PIPE));
-            }
+            const int nx = st + 1 < last ? st + 1 : last;
+            // the slot's reads have returned before its refill is issued
+            __builtin_amdgcn_sched_barrier(0);
+            wait_lgkmcnt0();
+            issue(nx, slot);
             if constexpr (Sh::WREG) {  // one stage ahead, into the other set
                 load_w(nx, wreg[(j + 1) % 2]);
             }
@@ -971,11 +914,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
         }
     }
     };
-    // (slots past PIPE are never named; they alias slot 0)
-    mainloop(xbuf, xbuf + (PIPE > 1 ? 1 : 0) * Sh::STAGE, xbuf + (PIPE > 2 ? 2 : 0) * Sh::STAGE,
-             xbuf + (PIPE > 3 ? 3 : 0) * Sh::STAGE, xbuf + (PIPE > 4 ? 4 : 0) * Sh::STAGE,
-             xbuf + (PIPE > 5 ? 5 : 0) * Sh::STAGE, xbuf + (PIPE > 6 ? 6 : 0) * Sh::STAGE,
-             xbuf + (PIPE > 7 ? 7 : 0) * Sh::STAGE, sbt);
+    mainloop(xbuf, sbt);
     // the loads issued past the last stage land before the LDS is reused for
     // the reduction or released with the workgroup
     wait_vmcnt<0>();
@@ -991,7 +930,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
         for (int r0 = 1; r0 < wk; r0 += Sh::RSLOTS) {  // workgroup-uniform
             const int r1 = r0 + Sh::RSLOTS < wk ? r0 + Sh::RSLOTS : wk;
             if (kw >= r0 && kw < r1) {
-                float *dst = red + (size_t)((kw - r0) * WF + fw) * REGS * 64 + lane;
+                float *dst = red + (size_t)(kw - r0) * REGS * 64 + lane;
 #pragma unroll
                 for (int a = 0; a < A; ++a)
 #pragma unroll
@@ -1002,7 +941,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
             __syncthreads();
             if (kw == 0) {
                 for (int src = r0; src < r1; ++src) {
-                    const float *sp = red + (size_t)((src - r0) * WF + fw) * REGS * 64 + lane;
+                    const float *sp = red + (size_t)(src - r0) * REGS * 64 + lane;
 #pragma unroll
                     for (int a = 0; a < A; ++a)
 #pragma unroll
@@ -1044,14 +983,14 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
-template <typename T, int BITS, int A, int C, int WK, int PIPE, int EPI, int WF = 1>
+template <typename T, int BITS, int A, int C, int WK, int EPI>
 __global__ __launch_bounds__(64 * WK)
-__attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<PIPE, A, C>()))) void qmm_mfma_kernel(
+__attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<A, C>()))) void qmm_mfma_kernel(
     QParams p) {
     constexpr int TN = (epi_parts(EPI) == 1) ? A : 1;
-    __shared__ __attribute__((aligned(16))) char lds[MfmaShape<T, BITS, A, C, WK, PIPE, WF>::LDS];
-    qmm_mfma_tile<T, BITS, A, C, WK, PIPE, EPI, WF>(p, lds, (int64_t)blockIdx.x * (32 * TN * WF),
-                                                    (int64_t)blockIdx.y * (32 * C));
+    __shared__ __attribute__((aligned(16))) char lds[MfmaShape<T, BITS, A, C, WK>::LDS];
+    qmm_mfma_tile<T, BITS, A, C, WK, EPI>(p, lds, (int64_t)blockIdx.x * (32 * TN),
+                                          (int64_t)blockIdx.y * (32 * C));
 }
 
 // Block i of a run of n feature tiles that take g workgroups each (the g
@@ -1086,12 +1025,12 @@ __device__ __forceinline__ void mixed_tile_of(int64_t i, int64_t n, int g, int64
 // Tiles never change the results (same K split and accumulation order).
 template <typename T, int BITS, int A, int EPI, int CB>
 __global__ __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<1, A, CB>()))) void qmm_mfma_mixed_kernel(
+__attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<A, CB>()))) void qmm_mfma_mixed_kernel(
     QParams p) {
     static_assert(CB == 4 || CB == 2, "128/64- or 64/32-token tiles");
     constexpr int CS = CB / 2, GB = 4 / CB, GS = 2 * GB;
     constexpr int TN = (epi_parts(EPI) == 1) ? A : 1;
-    constexpr int LB = MfmaShape<T, BITS, A, CB, 4, 1>::LDS, LS = MfmaShape<T, BITS, A, CS, 4, 1>::LDS;
+    constexpr int LB = MfmaShape<T, BITS, A, CB, 4>::LDS, LS = MfmaShape<T, BITS, A, CS, 4>::LDS;
     __shared__ __attribute__((aligned(16))) char lds[LB > LS ? LB : LS];
     const int64_t b = blockIdx.x, nb = p.n4;
     const int64_t nt = (p.Nout + 32 * TN - 1) / (32 * TN);
@@ -1102,16 +1041,16 @@ __attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<1, A, CB>()))) void qmm_mfm
         // instead of 29.5-29.7 us, A/B on one box, with an identical main
         // loop; the cause was not found)
         if (b < nb) {
-            qmm_mfma_tile<T, BITS, A, CB, 4, 1, EPI, 1>(p, lds, b * (32 * TN), 0);
+            qmm_mfma_tile<T, BITS, A, CB, 4, EPI>(p, lds, b * (32 * TN), 0);
             return;
         }
     } else if (b < nb * GB) {
         mixed_tile_of(b, nb, GB, j, part);
-        qmm_mfma_tile<T, BITS, A, CB, 4, 1, EPI, 1>(p, lds, j * (32 * TN), part * 32 * CB);
+        qmm_mfma_tile<T, BITS, A, CB, 4, EPI>(p, lds, j * (32 * TN), part * 32 * CB);
         return;
     }
     mixed_tile_of(b - nb * GB, nt - nb, GS, j, part);
-    qmm_mfma_tile<T, BITS, A, CS, 4, 1, EPI, 1>(p, lds, (nb + j) * (32 * TN), part * 32 * CS);
+    qmm_mfma_tile<T, BITS, A, CS, 4, EPI>(p, lds, (nb + j) * (32 * TN), part * 32 * CS);
 }
 
 // ---------------------------------------------------------------------------
@@ -1137,16 +1076,14 @@ int launch_qmv(const QParams &p, hipStream_t st) {
 // tables (dynamic).
 template <typename T, int BITS, int A, int C>
 int64_t mfma_lds_bytes(const QParams &p, int wk) {
-    constexpr int PIPE = mfma_pipe<T, BITS, A, C>();
     const SbtLayout tl = sbt_layout(p.K / wk, p.gs);
-    return MfmaShape<T, BITS, A, C, 4, PIPE>::LDS + (int64_t)wk * A * 2 * tl.array_bytes;
+    return MfmaShape<T, BITS, A, C, 4>::LDS + (int64_t)wk * A * 2 * tl.array_bytes;
 }
 
 template <typename T, int BITS, int A, int C, int EPI>
 int launch_mfma_cfg(QParams p, int wk, hipStream_t st) {
     constexpr int P = epi_parts(EPI);
     constexpr int TN = (P == 1) ? A : 1;
-    constexpr int PIPE = mfma_pipe<T, BITS, A, C>();
     p.wk = wk;
     const SbtLayout tl = sbt_layout(p.K / wk, p.gs);
     p.sbp = tl.pitch;
@@ -1155,7 +1092,7 @@ int launch_mfma_cfg(QParams p, int wk, hipStream_t st) {
         return fail(MI_ERR_UNSUPPORTED, "quantized matmul tile exceeds the LDS (K = %lld)",
                     (long long)p.K);
     const dim3 grid((unsigned)ceil_div(p.Nout, 32 * TN), (unsigned)ceil_div(p.M, 32 * C));
-    qmm_mfma_kernel<T, BITS, A, C, 4, PIPE, EPI><<<grid, 64 * wk, dyn, st>>>(p);
+    qmm_mfma_kernel<T, BITS, A, C, 4, EPI><<<grid, 64 * wk, dyn, st>>>(p);
     return launch_status("quantized matmul (mfma)");
 }
 
@@ -1231,8 +1168,7 @@ int launch_mfma(const QParams &p, hipStream_t st) {
     // Aiming at one per CU does not pay: q/k/v at M = 128 with 128/64-token
     // tiles, 384 -> 256 workgroups, went 15.2 -> 15.4 us; a lone larger
     // workgroup takes as long as two smaller ones sharing a CU.
-    if constexpr (BITS == 4 && P <= 2 && mfma_pipe<T, BITS, P, 4>() == 1 &&
-                  mfma_pipe<T, BITS, P, 2>() == 1 && mfma_pipe<T, BITS, P, 1>() == 1) {
+    if constexpr (BITS == 4 && P <= 2) {
         const int64_t cus = device_cus();
         if (p.M > 64 && p.M <= 128 && wk == 4) {
             if constexpr (P == 2) {

@@ -433,29 +433,33 @@ def _qmm_auto(x, lin, gs, bits, dtype):
     return quantized_matmul(x, wq, s, b, gs, bits, dtype)
 
 
-def qwen3_layer(x, W: dict, cfg, offset: int, kcache, vcache, dtype: str = "bfloat16"):
+def qwen3_layer(x, W: dict, cfg, offset: int, kcache, vcache, dtype: str = "bfloat16",
+                qmm=None):
     """One Qwen3 decoder layer (mlx-lm qwen3.py order): h = x + attn(norm(x)),
     out = h + mlp(norm(h)). W holds (wq, scales, biases) per projection and norm
     weights; kcache/vcache [1, HK, cap, D] float32 are written at
-    [offset, offset + L). Returns the layer output [1, L, hidden]."""
+    [offset, offset + L). Returns the layer output [1, L, hidden].
+    qmm(x, lin) -> projection replaces the default routing (_qmm_auto); the
+    CPU baseline passes the C factored restatement for every projection."""
     gs, bits, eps = cfg.group_size, cfg.bits, cfg.rms_norm_eps
+    proj = qmm or (lambda a, lin: _qmm_auto(a, lin, gs, bits, dtype))
     H, HK, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
     L = x.shape[1]
     xn = rms_norm(x, W["input_layernorm"], eps, dtype)
-    q = _qmm_auto(xn, W["q_proj"], gs, bits, dtype)
-    k = _qmm_auto(xn, W["k_proj"], gs, bits, dtype)
-    v = _qmm_auto(xn, W["v_proj"], gs, bits, dtype)
+    q = proj(xn, W["q_proj"])
+    k = proj(xn, W["k_proj"])
+    v = proj(xn, W["v_proj"])
     qr = norm_rope(q, W["q_norm"], eps, H, D, cfg.rope_theta, offset, dtype)
     kcache[:, :, offset:offset + L] = norm_rope(k, W["k_norm"], eps, HK, D, cfg.rope_theta,
                                                 offset, dtype)
     vcache[:, :, offset:offset + L] = norm_rope(v, None, 0.0, HK, 0, 1.0, 0, dtype)
     o = sdpa(qr, kcache[:, :, :offset + L], vcache[:, :, :offset + L], D ** -0.5, L > 1, dtype)
     o = np.ascontiguousarray(np.transpose(o, (0, 2, 1, 3))).reshape(1, L, H * D)
-    h = round_to(x.astype(np.float64) + _qmm_auto(o, W["o_proj"], gs, bits, dtype), dtype)
+    h = round_to(x.astype(np.float64) + proj(o, W["o_proj"]), dtype)
     hn = rms_norm(h, W["post_attention_layernorm"], eps, dtype)
-    g = _qmm_auto(hn, W["gate_proj"], gs, bits, dtype)
-    u = _qmm_auto(hn, W["up_proj"], gs, bits, dtype)
-    d = _qmm_auto(swiglu(g, u, dtype), W["down_proj"], gs, bits, dtype)
+    g = proj(hn, W["gate_proj"])
+    u = proj(hn, W["up_proj"])
+    d = proj(swiglu(g, u, dtype), W["down_proj"])
     return round_to(h.astype(np.float64) + d, dtype)
 
 

@@ -549,3 +549,18 @@ def test_norm_rope_permuting_heads_permutes_outputs():
     np.testing.assert_array_equal(
         one[:, 0], oracle.rope(oracle.rms_norm(x[:, :, 0], w, 1e-6, "bfloat16"), D, False, 1e6,
                                1.0, 2, "bfloat16"))
+
+
+def test_layer_with_factored_projections_stays_within_the_bar():
+    """The CPU baseline's layer (every projection through the C factored qmm)
+    against the default oracle layer (dequantize-then-matmul at M > 8)."""
+    cfg, W = _tiny_layer(31)
+    x = oracle.round_to(rng(32).normal(0, 1, (1, 24, 128)), "bfloat16")
+    kc = np.zeros((1, cfg.num_key_value_heads, 24, cfg.head_dim), np.float32)
+
+    def proj(a, lin):
+        return oracle.qmm_factored(a, *lin, cfg.group_size, cfg.bits, "bfloat16")
+
+    a = oracle.qwen3_layer(x, W, cfg, 0, kc.copy(), kc.copy(), qmm=proj)
+    b = oracle.qwen3_layer(x, W, cfg, 0, kc.copy(), kc.copy())
+    assert np.abs(a - b).max() <= 1e-2 * np.abs(b).max()
