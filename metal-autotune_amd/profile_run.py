@@ -13,7 +13,11 @@ Runs, eagerly on the current stream:
    64) rotating over enough weight sets that they cannot stay in the 256 MB
    Infinity Cache -- the same kernel and shape bench.py reports in
    ``roofline``;
-3. the same for a plain qmm at M = 1 (decode GEMV, [9728, 2560]).
+3. the same for a plain qmm at M = 1 (decode GEMV, [9728, 2560]);
+4. the two narrow projections of the layer with their residual epilogue
+   (``ops.qmm_residual``, the [qmm, add] region): o_proj (x[128, 4096] @
+   [2560, 4096]^T) and down_proj (x[128, 9728] @ [2560, 9728]^T), each over
+   enough weight copies to exceed the Infinity Cache.
 
 Prints one line per phase so the counter rows can be matched to phases by
 kernel name and launch order.
@@ -68,6 +72,19 @@ def main():
         ops.quantized_matmul(x1, *ws[i % sets][i % 2])
     torch.cuda.synchronize()
     print(f"phase gemv: {args.reps} x qmm M=1 N={N} K={K}", flush=True)
+    del ws
+
+    for name, n_out, k_in in (("o_proj", 2560, 4096), ("down_proj", 2560, 9728)):
+        per = n_out * k_in * 9 // 16
+        copies = (300 << 20) // per + 1
+        wsn = [random_quantized(n_out, k_in, gen, "cuda") for _ in range(copies)]
+        xin = torch.randn((1, M, k_in), generator=gen, device="cuda").to(torch.bfloat16)
+        res = torch.randn((1, M, n_out), generator=gen, device="cuda").to(torch.bfloat16)
+        for i in range(args.reps):
+            ops.qmm_residual(xin, *wsn[i % copies], res)
+        torch.cuda.synchronize()
+        print(f"phase {name}: {args.reps} x qmm+residual M={M} N={n_out} K={k_in}", flush=True)
+        del wsn
 
 
 if __name__ == "__main__":
