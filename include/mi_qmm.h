@@ -36,8 +36,8 @@
 extern "C" {
 #endif
 
-#define MI_ABI_VERSION 4  /* 2: mi_argmax takes a workspace; 3: mi_gelu_mlp_f32;
-                             4: mi_argmax_noalloc */
+#define MI_ABI_VERSION 5  /* 2: mi_argmax takes a workspace; 3: mi_gelu_mlp_f32;
+                             4: mi_argmax_noalloc; 5: the qmm workspace entries */
 
 enum mi_dtype { MI_F32 = 0, MI_F16 = 1, MI_BF16 = 2 };
 
@@ -99,6 +99,38 @@ int mi_qmm_affine_residual_rmsnorm(const void *x, const uint32_t *w, const void 
                                    const void *norm_w, float eps, void *h, void *y,
                                    int64_t M, int64_t N, int64_t K, int group_size, int bits,
                                    int dtype, void *stream);
+
+/* K parts. On the MFMA path (16-bit T, 8 < M <= 128, K >= 4096) the
+ * accumulation over K is cut into 2 (K < 8192) or 4 parts, each split over
+ * four waves of a workgroup, and the parts are added in order -- one fixed
+ * order per (M, K), whichever entry point or tile computes the output.
+ * Without a workspace a workgroup runs the parts in turn. The _ws entries run
+ * them as workgroups of their own, into a caller-owned fp32 workspace of
+ * mi_qmm_workspace_bytes(...) bytes (16-byte aligned; contents need no
+ * initialization), and a second kernel adds them and applies the region's
+ * epilogue: the same results, bit for bit, on narrow-N projections (o_proj,
+ * down_proj at prefill sizes) that otherwise fill a fraction of the GPU.
+ * A NULL, short or misaligned workspace, or a shape with one K part, takes
+ * the entry without _ws. Calls sharing a workspace must not overlap.
+ * Same operations as mi_qmm_affine, mi_qmm_affine_residual and
+ * mi_qmm_affine_residual_rmsnorm (kernels.py:193-220 call sites). MLX itself
+ * splits K for small tile counts (qmm_splitk, whose count the reference
+ * restates at scaffold/stitch.py:91-100); these parts are this library's own. */
+int64_t mi_qmm_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                               int dtype);  /* 0: no K parts at this shape */
+int mi_qmm_affine_ws(const void *x, const uint32_t *w, const void *scales, const void *biases,
+                     void *y, int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                     int dtype, void *workspace, int64_t workspace_bytes, void *stream);
+int mi_qmm_affine_residual_ws(const void *x, const uint32_t *w, const void *scales,
+                              const void *biases, const void *resid, void *y, int64_t M,
+                              int64_t N, int64_t K, int group_size, int bits, int dtype,
+                              void *workspace, int64_t workspace_bytes, void *stream);
+int mi_qmm_affine_residual_rmsnorm_ws(const void *x, const uint32_t *w, const void *scales,
+                                      const void *biases, const void *resid,
+                                      const void *norm_w, float eps, void *h, void *y,
+                                      int64_t M, int64_t N, int64_t K, int group_size,
+                                      int bits, int dtype, void *workspace,
+                                      int64_t workspace_bytes, void *stream);
 
 /* Region [qmm, split(3), mul]: t = x @ dequant(w)^T with w of 3*D rows;
  * B, C, xs = split(t, 3, axis=-1); c_out = C, bx_out = T(B * xs)

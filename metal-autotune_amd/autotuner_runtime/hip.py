@@ -23,7 +23,7 @@ import torch
 
 PKG = Path(__file__).resolve().parent.parent
 LIB_PATH = Path(os.environ.get("MI_QMM_LIB", PKG / "libmiqmm.so"))
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 MI_F32, MI_F16, MI_BF16 = 0, 1, 2
 MI_OK, MI_ERR_ARG, MI_ERR_UNSUPPORTED, MI_ERR_LAUNCH = 0, 1, 2, 3
@@ -42,6 +42,12 @@ SIGNATURES: dict[str, list] = {
     "mi_qmm_affine_residual": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _I, _P],
     "mi_qmm_affine_residual_rmsnorm": [_P, _P, _P, _P, _P, _P, _F, _P, _P, _I64, _I64, _I64,
                                        _I, _I, _I, _P],
+    "mi_qmm_workspace_bytes": [_I64, _I64, _I64, _I, _I, _I],
+    "mi_qmm_affine_ws": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _I, _P, _I64, _P],
+    "mi_qmm_affine_residual_ws": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _I, _P,
+                                  _I64, _P],
+    "mi_qmm_affine_residual_rmsnorm_ws": [_P, _P, _P, _P, _P, _P, _F, _P, _P, _I64, _I64,
+                                          _I64, _I, _I, _I, _P, _I64, _P],
     "mi_qmm_affine_split_gate": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _I, _P],
     "mi_qmm_affine_dual": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _I, _I,
                            _I, _P],
@@ -62,7 +68,8 @@ SIGNATURES: dict[str, list] = {
     "mi_argmax_noalloc": [_P, _P, _I64, _I64, _I, _P],
 }
 RESTYPES = {"mi_last_error": ctypes.c_char_p, "mi_argmax_workspace_bytes": ctypes.c_int64,
-            "mi_gelu_mlp_f32_workspace_bytes": ctypes.c_int64}
+            "mi_gelu_mlp_f32_workspace_bytes": ctypes.c_int64,
+            "mi_qmm_workspace_bytes": ctypes.c_int64}
 
 _lock = threading.Lock()
 _lib = None
@@ -205,6 +212,15 @@ def _out_like(y, x, N, name="output"):
         raise ValueError(f"{name} must be {x.dtype} {(*x.shape[:-1], N)}, got {y.dtype} {tuple(y.shape)}")
 
 
+def _qmm_workspace(x, M, N, K, gs, bits, dt):
+    """The K-part workspace of the _ws entries at this shape, or None (one
+    K part: the plain entry)."""
+    nbytes = int(lib().mi_qmm_workspace_bytes(M, N, K, gs, bits, dt))
+    if nbytes == 0:
+        return None
+    return _workspace("qmm", x.device, _stream(x), nbytes, 8 << 20)
+
+
 def b_qmm(ins, outs, p):
     x, w, s, b = ins
     (y,) = outs
@@ -213,6 +229,12 @@ def b_qmm(ins, outs, p):
     M, N, K, gs, bits = _qmm_dims(x, w, s, b, p)
     dt = _act_dtype(x, s)
     _out_like(y, x, N)
+    ws = _qmm_workspace(x, M, N, K, gs, bits, dt)
+    if ws is not None:
+        _check(lib().mi_qmm_affine_ws(_ptr(x), _ptr(w), _ptr(s), _ptr(b), _ptr(y), M, N, K, gs,
+                                      bits, dt, _ptr(ws), ws.numel(), _stream(x)),
+               "quantized matmul")
+        return
     _check(lib().mi_qmm_affine(_ptr(x), _ptr(w), _ptr(s), _ptr(b), _ptr(y), M, N, K, gs, bits, dt,
                                _stream(x)), "quantized matmul")
 
@@ -226,6 +248,12 @@ def b_qmm_residual(ins, outs, p):
     dt = _act_dtype(x, s)
     _out_like(y, x, N)
     _out_like(r, x, N, "residual")
+    ws = _qmm_workspace(x, M, N, K, gs, bits, dt)
+    if ws is not None:
+        _check(lib().mi_qmm_affine_residual_ws(_ptr(x), _ptr(w), _ptr(s), _ptr(b), _ptr(r),
+                                               _ptr(y), M, N, K, gs, bits, dt, _ptr(ws),
+                                               ws.numel(), _stream(x)), "qmm + residual")
+        return
     _check(lib().mi_qmm_affine_residual(_ptr(x), _ptr(w), _ptr(s), _ptr(b), _ptr(r), _ptr(y), M,
                                         N, K, gs, bits, dt, _stream(x)), "qmm + residual")
 
@@ -241,6 +269,13 @@ def b_qmm_residual_rmsnorm(ins, outs, p):
         _out_like(t, x, N, name)
     if tuple(nw.shape) != (N,) or nw.dtype != x.dtype:
         raise ValueError(f"norm weight must be {x.dtype} [{N}]")
+    ws = _qmm_workspace(x, M, N, K, gs, bits, dt)
+    if ws is not None:
+        _check(lib().mi_qmm_affine_residual_rmsnorm_ws(
+            _ptr(x), _ptr(w), _ptr(s), _ptr(b), _ptr(r), _ptr(nw), float(p["eps"]), _ptr(h),
+            _ptr(y), M, N, K, gs, bits, dt, _ptr(ws), ws.numel(), _stream(x)),
+            "qmm + residual + rms_norm")
+        return
     _check(lib().mi_qmm_affine_residual_rmsnorm(_ptr(x), _ptr(w), _ptr(s), _ptr(b), _ptr(r),
                                                 _ptr(nw), float(p["eps"]), _ptr(h), _ptr(y), M,
                                                 N, K, gs, bits, dt, _stream(x)),
@@ -403,15 +438,22 @@ def b_linear_f32(ins, outs, p):
 # Workspaces of mi_gelu_mlp_f32 per (device, stream): their ticket counters
 # start at zero (torch.zeros) and every call leaves them zero, so one buffer
 # serves every later call on that stream (calls on one stream never overlap).
-_mlp_workspaces: dict[tuple, torch.Tensor] = {}
+# Workspaces per (kind, device, stream), zero-filled when made. Calls on one
+# stream run in order, so they share it. A workspace that has to grow is
+# replaced and the old one kept alive: a HIP graph captured with it still
+# addresses it.
+_workspaces: dict[tuple, torch.Tensor] = {}
+_retired: list[torch.Tensor] = []
 
 
-def _mlp_workspace(device, stream: int, nbytes: int) -> torch.Tensor:
-    key = (device, stream)
-    ws = _mlp_workspaces.get(key)
+def _workspace(kind: str, device, stream: int, nbytes: int, minimum: int = 4096) -> torch.Tensor:
+    key = (kind, device, stream)
+    ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 4096), dtype=torch.uint8, device=device)
-        _mlp_workspaces[key] = ws
+        if ws is not None:
+            _retired.append(ws)
+        ws = torch.zeros(max(nbytes, minimum), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
     return ws
 
 
@@ -432,7 +474,7 @@ def b_gelu_mlp_f32(ins, outs, p):
         raise ValueError("gelu_mlp_f32 shapes")
     stream = _stream(x)
     nbytes = int(lib().mi_gelu_mlp_f32_workspace_bytes(M, K, H, N))
-    ws = _mlp_workspace(x.device, stream, nbytes)
+    ws = _workspace("gelu_mlp", x.device, stream, nbytes)
     _check(lib().mi_gelu_mlp_f32(_ptr(x), _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2), _ptr(y), M, K,
                                  H, N, _ptr(ws), ws.numel(), stream), "gelu_mlp_f32")
 

@@ -12,6 +12,9 @@ namespace mi {
 int qmm_residual_launch(const void *x, const uint32_t *w, const void *s, const void *b,
                         const void *resid, void *y, int64_t M, int64_t N, int64_t K, int gs,
                         int bits, int dtype, void *stream);
+int64_t qmm_parts_bytes(int64_t M, int64_t N, int64_t K, int gs, int bits, int dtype);
+int qmm_parts_launch(const void *x, const uint32_t *w, const void *s, const void *b, float *part,
+                     int64_t M, int64_t N, int64_t K, int gs, int bits, int dtype, void *stream);
 
 namespace {
 
@@ -71,26 +74,14 @@ __global__ __launch_bounds__(256) void rms_kernel(const T *__restrict__ x, const
 // thread, then a fixed-order reduction (xor tree in each wave, waves 0..3).
 constexpr int RMS_RC = 2;  // 16-byte chunks per thread
 
+// The normalization of one row whose 16-byte chunks c = threadIdx.x + 256 i
+// (c < nc) this thread holds in xv, with the weight chunks in wv.
 template <typename T>
-__global__ __launch_bounds__(256) void rms_row_kernel(const T *__restrict__ x,
-                                                      const T *__restrict__ w, T *__restrict__ y,
-                                                      int64_t D, float eps) {
+__device__ __forceinline__ void rms_row_store(const uint4 (&xv)[RMS_RC],
+                                              const uint4 (&wv)[RMS_RC], T *__restrict__ yr,
+                                              int nc, int64_t D, float eps) {
     __shared__ float part[4];
-    const int64_t row = blockIdx.x;
-    const T *xr = x + row * D;
-    T *yr = y + row * D;
-    const int nc = (int)(D / 8);
-    uint4 xv[RMS_RC], wv[RMS_RC];
     float ss = 0.0f;
-    // the weight is loaded with the row, not after the reduction: one memory
-    // round trip per launch instead of two
-#pragma unroll
-    for (int i = 0; i < RMS_RC; ++i) {
-        const int c = threadIdx.x + 256 * i;
-        const int cc = c < nc ? c : nc - 1;  // clamped: in bounds, unused past nc
-        xv[i] = ld16(xr + 8 * cc);
-        wv[i] = ld16(w + 8 * cc);
-    }
 #pragma unroll
     for (int i = 0; i < RMS_RC; ++i) {
         if (threadIdx.x + 256 * i < nc) {
@@ -120,12 +111,82 @@ __global__ __launch_bounds__(256) void rms_row_kernel(const T *__restrict__ x,
 }
 
 template <typename T>
+__global__ __launch_bounds__(256) void rms_row_kernel(const T *__restrict__ x,
+                                                      const T *__restrict__ w, T *__restrict__ y,
+                                                      int64_t D, float eps) {
+    const int64_t row = blockIdx.x;
+    const T *xr = x + row * D;
+    const int nc = (int)(D / 8);
+    uint4 xv[RMS_RC], wv[RMS_RC];
+    // the weight is loaded with the row, not after the reduction: one memory
+    // round trip per launch instead of two
+#pragma unroll
+    for (int i = 0; i < RMS_RC; ++i) {
+        const int c = threadIdx.x + 256 * i;
+        const int cc = c < nc ? c : nc - 1;  // clamped: in bounds, unused past nc
+        xv[i] = ld16(xr + 8 * cc);
+        wv[i] = ld16(w + 8 * cc);
+    }
+    rms_row_store<T>(xv, wv, y + row * D, nc, D, eps);
+}
+
+// [qmm, add, rms_norm] after a K-part launch: row m of h is
+// T(resid + T(sum of the ks fp32 parts, in part order)), the [qmm, add]
+// epilogue, and the normalized row is rms_row_kernel's on that h (the same
+// chunks per thread, so the same sums). One workgroup per row.
+template <typename T>
+__global__ __launch_bounds__(256) void rms_parts_kernel(const float *__restrict__ part, int ks,
+                                                        const T *__restrict__ resid,
+                                                        const T *__restrict__ w,
+                                                        T *__restrict__ h, T *__restrict__ y,
+                                                        int64_t M, int64_t D, float eps) {
+    const int64_t row = blockIdx.x;
+    const int nc = (int)(D / 8);
+    uint4 xv[RMS_RC], wv[RMS_RC];
+#pragma unroll
+    for (int i = 0; i < RMS_RC; ++i) {
+        const int c = threadIdx.x + 256 * i;
+        const int cc = c < nc ? c : nc - 1;  // clamped: in bounds, unused past nc
+        const int64_t o = row * D + 8 * cc;
+        wv[i] = ld16(w + 8 * cc);
+        const uint4 rv = ld16(resid + o);
+        float4 lo = *(const float4 *)(part + o), hi = *(const float4 *)(part + o + 4);
+        float s[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        for (int z = 1; z < ks; ++z) {
+            lo = *(const float4 *)(part + z * M * D + o);
+            hi = *(const float4 *)(part + z * M * D + o + 4);
+            s[0] += lo.x;
+            s[1] += lo.y;
+            s[2] += lo.z;
+            s[3] += lo.w;
+            s[4] += hi.x;
+            s[5] += hi.y;
+            s[6] += hi.z;
+            s[7] += hi.w;
+        }
+        float f[8];
+        unpack8<T>(rv, f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = f[e] + (float)cvt<T>(s[e]);
+        xv[i] = pack8<T>(f);
+        if (c < nc) st16(h + o, xv[i]);
+    }
+    rms_row_store<T>(xv, wv, y + row * D, nc, D, eps);
+}
+
+// rms_row_kernel's shapes: 16-bit rows of 1024..4096 values, 16-byte aligned
+inline bool rms_row_ok(int64_t D, const void *x, const void *w, const void *y) {
+    return D % 8 == 0 && D >= 1024 && D <= 8 * 256 * RMS_RC && aligned(x, 16) && aligned(w, 16) &&
+           aligned(y, 16);
+}
+
+template <typename T>
 int launch_rms(const void *x, const void *w, void *y, int64_t rows, int64_t D, float eps,
                hipStream_t st) {
     if (rows == 0) return MI_OK;
     const int vec = D % 8 == 0 && aligned(x, 16) && aligned(w, 16) && aligned(y, 16);
     if constexpr (sizeof(T) == 2) {
-        if (vec && D >= 1024 && D <= 8 * 256 * RMS_RC) {
+        if (rms_row_ok(D, x, w, y)) {
             rms_row_kernel<T><<<(unsigned)rows, 256, 0, st>>>((const T *)x, (const T *)w,
                                                               (T *)y, D, eps);
             return launch_status("rms_norm");
@@ -276,6 +337,36 @@ extern "C" int mi_qmm_affine_residual_rmsnorm(const void *x, const uint32_t *w,
         return e;
     if (M == 0 || N == 0) return MI_OK;
     return rms_launch(h, norm_w, y, M, N, eps, dtype, stream);
+}
+
+extern "C" int mi_qmm_affine_residual_rmsnorm_ws(const void *x, const uint32_t *w,
+                                                 const void *scales, const void *biases,
+                                                 const void *resid, const void *norm_w, float eps,
+                                                 void *h, void *y, int64_t M, int64_t N, int64_t K,
+                                                 int group_size, int bits, int dtype,
+                                                 void *workspace, int64_t workspace_bytes,
+                                                 void *stream) {
+    const int64_t need = qmm_parts_bytes(M, N, K, group_size, bits, dtype);
+    if (need == 0 || !workspace || workspace_bytes < need || !aligned(workspace, 16) ||
+        !rms_row_ok(N, h, norm_w, y) || !aligned(resid, 16))
+        return mi_qmm_affine_residual_rmsnorm(x, w, scales, biases, resid, norm_w, eps, h, y, M,
+                                              N, K, group_size, bits, dtype, stream);
+    if (!norm_w || !y || !h || !resid)
+        return fail(MI_ERR_ARG, "null norm weight, output or residual");
+    if (int e = qmm_parts_launch(x, w, scales, biases, (float *)workspace, M, N, K, group_size,
+                                 bits, dtype, stream))
+        return e;
+    const int ks = (int)(need / (M * N * (int64_t)sizeof(float)));
+    hipStream_t st = as_stream(stream);
+    if (dtype == MI_BF16)
+        rms_parts_kernel<bf16><<<(unsigned)M, 256, 0, st>>>(
+            (const float *)workspace, ks, (const bf16 *)resid, (const bf16 *)norm_w, (bf16 *)h,
+            (bf16 *)y, M, N, eps);
+    else
+        rms_parts_kernel<f16><<<(unsigned)M, 256, 0, st>>>(
+            (const float *)workspace, ks, (const f16 *)resid, (const f16 *)norm_w, (f16 *)h,
+            (f16 *)y, M, N, eps);
+    return launch_status("qmm + residual + rms_norm (sum of K parts)");
 }
 
 namespace mi {

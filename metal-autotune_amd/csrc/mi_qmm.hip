@@ -57,7 +57,23 @@ struct QParams {
     int wk;                    // K-split waves (qmm_mfma_kernel)
     int sbp;                   // qmm_mfma_kernel: groups per row of a wave's scale/bias table
     int n4;                    // qmm_mfma_mixed_kernel: feature tiles taken as 128-token tiles
+    int ks;                    // K parts (kpart_count): each is split over the wk waves
+    int kslice;                // k values of the longest wave chunk (ks * wk chunks of K)
+    float *part;               // non-null: write K part blockIdx.z's sums, fp32 [ks, M, Nout]
 };
+
+// K parts of the MFMA path: a function of (M, K) alone, so every entry point
+// and epilogue (and the tile shape) gives an output element the same sums in
+// the same order. Narrow-N projections at prefill sizes (o_proj, down_proj:
+// N = 2560, K = 4096 / 9728, M = 128) otherwise fill 160-320 workgroups,
+// each wave streaming 16-38 stages one after another. With a workspace the
+// parts run as workgroups of their own (grid z) and a second kernel adds them
+// in part order; without one a workgroup runs its parts in turn (qmm_mfma_tile)
+// and the sums are the same.
+inline int kpart_count(int64_t M, int64_t K) {
+    if (M <= 8 || M > 128 || K < 4096) return 1;
+    return K >= 8192 ? 4 : 2;
+}
 
 template <typename T> __device__ __forceinline__ float swiglu1(float g, float u) {
     const float gt = (float)cvt<T>(g);
@@ -621,10 +637,22 @@ template <int A, int C> constexpr int mfma_waves_per_eu() {
 // One workgroup's tile: tokens [m_blk, m_blk + 32 * C) of the output features
 // starting at n_blk (32 * TN of them, per part). lds is the workgroup's static
 // LDS, at least MfmaShape::LDS bytes; the scale/bias tables live in the
-// dynamic LDS.
-template <typename T, int BITS, int A, int C, int WK, int EPI>
+// dynamic LDS, followed (p.ks > 1 without p.part) by the running sums over
+// the K parts, mfma_sum_bytes.
+//
+// K is cut into p.ks * wk chunks of whole 64-value stages, chunk c covering
+// stages [c T / chunks, (c + 1) T / chunks) of the T; K part z is chunks
+// z wk .. z wk + wk - 1, wave kw taking chunk z wk + kw. A part's sum is
+// ((c0 + c1) + c2) + c3 over its waves' chunks (the LDS reduction), and the
+// output sums the parts in order, (part 0 + part 1) + .... With p.part the
+// workgroup runs the one part kz and stores its sum; otherwise it runs every
+// part in turn. KM selects the case at compile time (KM_ONE: ks == 1, the
+// loop and its running sums compile away).
+enum KMode { KM_ONE = 0, KM_LOOP = 1, KM_PART = 2 };
+
+template <typename T, int BITS, int A, int C, int WK, int EPI, int KM = KM_ONE>
 __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64_t n_blk,
-                                              int64_t m_blk) {
+                                              int64_t m_blk, int kz = 0) {
     // The body uses gfx950 buffer resources, which the host target cannot
     // type; the host pass needs only the kernels' launch stubs.
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -638,16 +666,15 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
     const int lane = threadIdx.x & 63;
     // the wave index is uniform per wave: in a scalar register, the x stage
     // base addresses and the DMA's LDS destinations (M0) need no VALU work.
-    // Wave kw owns the K slice kw of the workgroup's wk.
+    // Wave kw owns chunk kw of each K part.
     const int kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = lane >> 5, r = lane & 31;
     const int64_t K = p.K, G = K / p.gs;
     int64_t n_wave = n_blk;
     const Bound bd = bind<EPI>(p, n_wave);
     const int wk = p.wk;
-    const int Kw = (int)(K / wk);
-    const int kbeg = kw * Kw;
-    const int nst = Kw / XK;
+    const int chunks = (KM == KM_ONE ? 1 : p.ks) * wk, nstages = (int)(K / XK);
+    const int nparts = KM == KM_LOOP ? p.ks : 1;  // K parts this workgroup runs
     char *xbuf = lds + kw * Sh::STAGE;
     const int wslot = Sh::XST;  // this wave's weights within its slot
 
@@ -672,33 +699,12 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
         br[a] = buffer_rsrc(bd.b(part), (uint32_t)(rows * G * 2));
         woff[a] = (uint32_t)(tile_row(a, r) * (K * BITS / 8) + 16 * h);
     }
-    // Scale/bias table (layout in sbt_layout): dword v of an array holds
-    // groups gbase + 2j, +1 of tile row v / (pitch / 2), j = v % (pitch / 2).
-    // Issued before the ring prologue, so the first stage's wait covers it.
     const int pitch = p.sbp;
-    const SbtLayout tl = sbt_layout(Kw, p.gs);
+    const SbtLayout tl = sbt_layout(p.kslice, p.gs);
     extern __shared__ __attribute__((aligned(16))) char lds_dyn[];
     const char *sbt = lds_dyn + kw * (A * 2 * tl.array_bytes);
-    const int gbase = (kbeg >> gshift) & ~1;
+    float *psum = (float *)(lds_dyn + wk * (A * 2 * tl.array_bytes));  // sums over K parts
     typedef __attribute__((address_space(3))) void *lds_ptr;
-    for (int i = 0; i < tl.ninst; ++i) {
-        int v = 64 * i + lane;
-        v = v < 16 * pitch ? v : 16 * pitch - 1;
-        const int rr = v / (pitch >> 1), j = v - rr * (pitch >> 1);
-#pragma unroll
-        for (int a = 0; a < A; ++a) {
-            const uint32_t off = (uint32_t)((tile_row(a, rr) * G + gbase + 2 * j) * 2);
-            char *dst = (char *)sbt + (2 * a) * tl.array_bytes + i * 256;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(sr[a], (lds_ptr)dst, 4, off, 0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(br[a], (lds_ptr)(dst + tl.array_bytes), 4, off,
-                                                     0, 0, 0);
-        }
-    }
-    // group of value k0 + h * VPC for a super-step start k0 (a multiple of
-    // 2 * VPC): k0 / gs, plus h when a group is no wider than a half-chunk;
-    // as a byte offset into the table, relative to gbase
-    const int hg = (p.gs <= VPC) ? h * (VPC >> gshift) : 0;
-    const int sbrow = (r * pitch + hg - gbase) * 2;
     // x DMA: instruction i writes stage rows 8i..8i+7; lane l fills row
     // 8i + l/8 at swizzled position l%8, i.e. it loads chunk (l%8) ^ swz(row).
     // Tokens past M point past
@@ -716,243 +722,316 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
                       ? (uint32_t)(((m_blk + row) * K + 8 * chunk) * (int64_t)sizeof(T))
                       : xbytes;
     }
-    auto issue = [&](int st, char *slot) {
-        const int k0 = kbeg + st * XK;
-        const uint32_t xs = (uint32_t)k0 * sizeof(T);
-#pragma unroll
-        for (int j = 0; j < Sh::XOPS; ++j)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(slot + j * 1024), 16, xoff[j], xs,
-                                                     0, 0);
-        if constexpr (Sh::WREG) return;
-#pragma unroll
-        for (int u = 0; u < SPS; ++u) {
-            const int ku = k0 + u * SS;
-            const uint32_t ws = (uint32_t)(ku / VPW) * 4;
-#pragma unroll
-            for (int a = 0; a < A; ++a) {
-                char *wdst = slot + wslot + (a * SPS + u) * 1024;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(wr[a], (lds_ptr)wdst, 16, woff[a], ws, 0, 0);
-            }
-        }
-    };
-    // WREG: the weight chunks of a stage into registers
-    uint4 wreg[2][A][SPS];
-    const char *wlane[A];
-#pragma unroll
-    for (int a = 0; a < A; ++a) {
-        const int part = (P == 1) ? 0 : a;
-        wlane[a] = (const char *)bd.w(part) + woff[a];
-    }
-    auto load_w = [&](int st, uint4 (&wd)[A][SPS]) {
-#pragma unroll
-        for (int u = 0; u < SPS; ++u) {
-            const int ku = kbeg + st * XK + u * SS;
-            const uint32_t ws = (uint32_t)(ku / VPW) * 4;
-#pragma unroll
-            for (int a = 0; a < A; ++a) {
-                wd[a][u] = ld16(wlane[a] + ws);
-            }
-        }
-    };
-
     f32x16 acc[A][C];
+    for (int kp = 0; kp < nparts; ++kp) {  // workgroup-uniform
+        const int cix = (KM == KM_PART ? kz : kp) * wk + kw;
+        const int sbeg = (int)((int64_t)cix * nstages / chunks);
+        const int kbeg = sbeg * XK;
+        const int nst = (int)((int64_t)(cix + 1) * nstages / chunks) - sbeg;
+        // Scale/bias table (layout in sbt_layout): dword v of an array holds
+        // groups gbase + 2j, +1 of tile row v / (pitch / 2), j = v % (pitch / 2).
+        // Issued before the ring prologue, so the first stage's wait covers it.
+        const int gbase = (kbeg >> gshift) & ~1;
+        for (int i = 0; i < tl.ninst; ++i) {
+            int v = 64 * i + lane;
+            v = v < 16 * pitch ? v : 16 * pitch - 1;
+            const int rr = v / (pitch >> 1), j = v - rr * (pitch >> 1);
 #pragma unroll
-    for (int a = 0; a < A; ++a)
+            for (int a = 0; a < A; ++a) {
+                const uint32_t off = (uint32_t)((tile_row(a, rr) * G + gbase + 2 * j) * 2);
+                char *dst = (char *)sbt + (2 * a) * tl.array_bytes + i * 256;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(sr[a], (lds_ptr)dst, 4, off, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(br[a], (lds_ptr)(dst + tl.array_bytes), 4, off,
+                                                         0, 0, 0);
+            }
+        }
+        // group of value k0 + h * VPC for a super-step start k0 (a multiple of
+        // 2 * VPC): k0 / gs, plus h when a group is no wider than a half-chunk;
+        // as a byte offset into the table, relative to gbase
+        const int hg = (p.gs <= VPC) ? h * (VPC >> gshift) : 0;
+        const int sbrow = (r * pitch + hg - gbase) * 2;
+        auto issue = [&](int st, char *slot) {
+            const int k0 = kbeg + st * XK;
+            const uint32_t xs = (uint32_t)k0 * sizeof(T);
 #pragma unroll
-        for (int c = 0; c < C; ++c)
+            for (int j = 0; j < Sh::XOPS; ++j)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(slot + j * 1024), 16, xoff[j], xs,
+                                                         0, 0);
+            if constexpr (Sh::WREG) return;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) acc[a][c][i] = 0.0f;
+            for (int u = 0; u < SPS; ++u) {
+                const int ku = k0 + u * SS;
+                const uint32_t ws = (uint32_t)(ku / VPW) * 4;
+#pragma unroll
+                for (int a = 0; a < A; ++a) {
+                    char *wdst = slot + wslot + (a * SPS + u) * 1024;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(wr[a], (lds_ptr)wdst, 16, woff[a], ws, 0, 0);
+                }
+            }
+        };
+        // WREG: the weight chunks of a stage into registers
+        uint4 wreg[2][A][SPS];
+        const char *wlane[A];
+#pragma unroll
+        for (int a = 0; a < A; ++a) {
+            const int part = (P == 1) ? 0 : a;
+            wlane[a] = (const char *)bd.w(part) + woff[a];
+        }
+        auto load_w = [&](int st, uint4 (&wd)[A][SPS]) {
+#pragma unroll
+            for (int u = 0; u < SPS; ++u) {
+                const int ku = kbeg + st * XK + u * SS;
+                const uint32_t ws = (uint32_t)(ku / VPW) * 4;
+#pragma unroll
+                for (int a = 0; a < A; ++a) {
+                    wd[a][u] = ld16(wlane[a] + ws);
+                }
+            }
+        };
 
-    // Pipeline: stage st reads the wave's slot into registers, waits for those
-    // reads, then refills the slot with stage st + 1 and computes while those
-    // DMAs fly. Every stage issues exactly OPS DMAs -- past the last stage
-    // they re-read stage nst - 1, in bounds, into the slot no later stage
-    // reads -- so at the top of a stage nothing else is in flight: vmcnt(0).
-    // The stage loop is unrolled twice so the two register weight sets are
-    // named statically.
-    //
-    // The slot and the scale/bias table are passed as separate __restrict__
-    // arguments of the inlined main loop: the resulting alias scopes let the
-    // compiler's wait-count pass see that a stage's table reads cannot touch
-    // the slot the DMAs in flight are filling, so it adds no vmcnt(0) of its
-    // own before them. The table's DMAs precede the prologue's, so the wait at
-    // the top of stage 0 retires them.
-    const int swz = (r >> 1) & 7;
-    const int tab = tl.array_bytes;
-    auto mainloop = [&](char *__restrict__ slot, const char *__restrict__ tb)
-                        __attribute__((always_inline)) {
-    const int last = nst > 0 ? nst - 1 : 0;
-    // Scales and biases of a stage are read from the table one stage ahead,
-    // so a stage's first dequant waits only for its weight chunk, not for the
-    // x fragments read before it (LDS reads complete in order).
-    uint32_t sq[A][SPS], bq[A][SPS];
-    auto load_sb = [&](int st) {
 #pragma unroll
         for (int a = 0; a < A; ++a)
 #pragma unroll
-            for (int u = 0; u < SPS; ++u) {
-                const char *sb = tb + 2 * a * tab + sbrow + ((kbeg + st * XK + u * SS) >> gshift) * 2;
-                sq[a][u] = *(const uint16_t *)sb;
-                bq[a][u] = *(const uint16_t *)(sb + tab);
-            }
-    };
-    issue(0, slot);
-    if constexpr (Sh::WREG) load_w(0, wreg[0]);
-    // the table's DMAs were issued before the prologue's
-    wait_vmcnt<Sh::TABLE_VMCNT>();
-    load_sb(0);
-    for (int st0 = 0; st0 < nst; st0 += Sh::UNROLL) {
+            for (int c = 0; c < C; ++c)
 #pragma unroll
-        for (int j = 0; j < Sh::UNROLL; ++j) {
-            const int st = st0 + j;
-            if (st >= nst) break;  // workgroup-uniform
-            wait_vmcnt<0>();
-            const char *cur = slot;
-            // the weight chunk first: the first dequant needs it, while the
-            // MFMAs that consume the x fragments come after that dequant
-            uint4 wq[A][SPS];
+                for (int i = 0; i < 16; ++i) acc[a][c][i] = 0.0f;
+
+        // Pipeline: stage st reads the wave's slot into registers, waits for those
+        // reads, then refills the slot with stage st + 1 and computes while those
+        // DMAs fly. Every stage issues exactly OPS DMAs -- past the last stage
+        // they re-read stage nst - 1, in bounds, into the slot no later stage
+        // reads -- so at the top of a stage nothing else is in flight: vmcnt(0).
+        // The stage loop is unrolled twice so the two register weight sets are
+        // named statically.
+        //
+        // The slot and the scale/bias table are passed as separate __restrict__
+        // arguments of the inlined main loop: the resulting alias scopes let the
+        // compiler's wait-count pass see that a stage's table reads cannot touch
+        // the slot the DMAs in flight are filling, so it adds no vmcnt(0) of its
+        // own before them. The table's DMAs precede the prologue's, so the wait at
+        // the top of stage 0 retires them.
+        const int swz = (r >> 1) & 7;
+        const int tab = tl.array_bytes;
+        auto mainloop = [&](char *__restrict__ slot, const char *__restrict__ tb)
+                            __attribute__((always_inline)) {
+        const int last = nst > 0 ? nst - 1 : 0;
+        // Scales and biases of a stage are read from the table one stage ahead,
+        // so a stage's first dequant waits only for its weight chunk, not for the
+        // x fragments read before it (LDS reads complete in order).
+        uint32_t sq[A][SPS], bq[A][SPS];
+        auto load_sb = [&](int st) {
 #pragma unroll
             for (int a = 0; a < A; ++a)
 #pragma unroll
                 for (int u = 0; u < SPS; ++u) {
-                    if constexpr (Sh::WREG)
-                        wq[a][u] = wreg[j % 2][a][u];
-                    else
-                        wq[a][u] = *(const uint4 *)(cur + wslot + (a * SPS + u) * 1024 + lane * 16);
+                    const char *sb = tb + 2 * a * tab + sbrow + ((kbeg + st * XK + u * SS) >> gshift) * 2;
+                    sq[a][u] = *(const uint16_t *)sb;
+                    bq[a][u] = *(const uint16_t *)(sb + tab);
                 }
-            __builtin_amdgcn_sched_barrier(0);
-            uint4 xf[C][SPS][S];
+        };
+        issue(0, slot);
+        if constexpr (Sh::WREG) load_w(0, wreg[0]);
+        // the table's DMAs were issued before the prologue's
+        wait_vmcnt<Sh::TABLE_VMCNT>();
+        load_sb(0);
+        for (int st0 = 0; st0 < nst; st0 += Sh::UNROLL) {
 #pragma unroll
-            for (int c = 0; c < C; ++c)
-#pragma unroll
-                for (int u = 0; u < SPS; ++u)
-#pragma unroll
-                    for (int s = 0; s < S; ++s) {
-                        const int chunk = (u * SS + h * VPC + 8 * s) >> 3;
-                        xf[c][u][s] =
-                            *(const uint4 *)(cur + (32 * c + r) * 128 + ((chunk ^ swz) << 4));
-                    }
-            // Group g = (u * S + s) * A + a is one 32-row x 16-k MFMA operand
-            // and its C MFMAs. 4-bit: group 0 is dequantized here, under the
-            // latency of the x reads, and every later group in slices between
-            // the MFMAs of the group before it (below). 8-bit keeps one
-            // dequant per group ahead of its MFMAs: its dequant is lighter,
-            // and the pipeline's extra live registers made the 128-token dual
-            // tile spill (M = 2048: 335 -> 395 us).
-            constexpr bool PIPED = BITS == 4;
-            typedef Dequant8<T, BITS> Dq;
-            auto dq_init = [&](Dq &d, int g) {
-                const int u = g / (S * A), s = (g / A) % S, a = g % A;
-                const uint32_t words[4] = {wq[a][u].x, wq[a][u].y, wq[a][u].z, wq[a][u].w};
-                d.init(BITS == 4 ? words[s] : words[2 * s], BITS == 4 ? 0u : words[2 * s + 1],
-                       (float)__builtin_bit_cast(T, (uint16_t)sq[a][u]),
-                       (float)__builtin_bit_cast(T, (uint16_t)bq[a][u]));
-            };
-            uint32_t opa[4];  // the next MFMA operand: four packed pairs
-            if constexpr (PIPED) {
-                Dq d;
-                dq_init(d, 0);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    opa[k] = d.pair(k);
-                    launder(opa[k]);  // computed here, not sunk to its MFMA
-                }
-            }
-            const int nx = st + 1 < last ? st + 1 : last;
-            // the slot's reads have returned before its refill is issued
-            __builtin_amdgcn_sched_barrier(0);
-            wait_lgkmcnt0();
-            issue(nx, slot);
-            if constexpr (Sh::WREG) {  // one stage ahead, into the other set
-                load_w(nx, wreg[(j + 1) % 2]);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            // Software pipeline: each MFMA of group g is followed by a slice
-            // of group g + 1's dequant (pair k after MFMA k * C / 4), so one
-            // wave issues its VALU while its MFMAs run. The laundered pairs
-            // and the fences keep instruction selection and the scheduler
-            // from clustering the MFMAs again (they did, four at a time,
-            // leaving the dequant exposed). Each accumulator still receives
-            // its MFMAs in K order: the results do not change.
-            constexpr int NG = SPS * S * A;
-#pragma unroll
-            for (int g = 0; g < NG; ++g) {
-                const int u = g / (S * A), s = (g / A) % S, a = g % A;
-                Dq d;
-                if constexpr (!PIPED) {
-                    dq_init(d, g);
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) opa[k] = d.pair(k);
-                }
-                const V8 af = __builtin_bit_cast(V8, (uint4){opa[0], opa[1], opa[2], opa[3]});
-                if constexpr (!PIPED) {
-#pragma unroll
-                    for (int c = 0; c < C; ++c)
-                        acc[a][c] = Mfma<T>::mma(af, __builtin_bit_cast(V8, xf[c][u][s]), acc[a][c]);
-                    continue;
-                }
-#pragma unroll
-                for (int c = 0; c < C; ++c) {
-                    acc[a][c] = Mfma<T>::mma(af, __builtin_bit_cast(V8, xf[c][u][s]), acc[a][c]);
-                    if (g + 1 < NG) {
-                        if (c == 0) {
-                            dq_init(d, g + 1);
-                            launder(d.a);
-                            launder(d.b);
-                        }
-#pragma unroll
-                        for (int k = 0; k < 4; ++k)
-                            if ((k * C) / 4 == c) {
-                                opa[k] = d.pair(k);
-                                launder(opa[k]);
-                            }
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-            }
-            load_sb(st < last ? st + 1 : last);
-        }
-    }
-    };
-    mainloop(xbuf, sbt);
-    // the loads issued past the last stage land before the LDS is reused for
-    // the reduction or released with the workgroup
-    wait_vmcnt<0>();
-
-    if constexpr (Sh::KG > 1) {
-        // Fixed-order reduction of the K-split partial tiles: K-group 0 adds
-        // groups 1, 2, ... in turn. The ring's LDS is reused, RSLOTS partials
-        // per round, so every wave must be done with its x stages first; all
-        // waves take part in every round's barriers.
-        constexpr int REGS = A * C * 16;
-        float *red = (float *)lds;
-        __syncthreads();
-        for (int r0 = 1; r0 < wk; r0 += Sh::RSLOTS) {  // workgroup-uniform
-            const int r1 = r0 + Sh::RSLOTS < wk ? r0 + Sh::RSLOTS : wk;
-            if (kw >= r0 && kw < r1) {
-                float *dst = red + (size_t)(kw - r0) * REGS * 64 + lane;
+            for (int j = 0; j < Sh::UNROLL; ++j) {
+                const int st = st0 + j;
+                if (st >= nst) break;  // workgroup-uniform
+                wait_vmcnt<0>();
+                const char *cur = slot;
+                // the weight chunk first: the first dequant needs it, while the
+                // MFMAs that consume the x fragments come after that dequant
+                uint4 wq[A][SPS];
 #pragma unroll
                 for (int a = 0; a < A; ++a)
 #pragma unroll
-                    for (int c = 0; c < C; ++c)
+                    for (int u = 0; u < SPS; ++u) {
+                        if constexpr (Sh::WREG)
+                            wq[a][u] = wreg[j % 2][a][u];
+                        else
+                            wq[a][u] = *(const uint4 *)(cur + wslot + (a * SPS + u) * 1024 + lane * 16);
+                    }
+                __builtin_amdgcn_sched_barrier(0);
+                uint4 xf[C][SPS][S];
 #pragma unroll
-                        for (int i = 0; i < 16; ++i) dst[((a * C + c) * 16 + i) * 64] = acc[a][c][i];
+                for (int c = 0; c < C; ++c)
+#pragma unroll
+                    for (int u = 0; u < SPS; ++u)
+#pragma unroll
+                        for (int s = 0; s < S; ++s) {
+                            const int chunk = (u * SS + h * VPC + 8 * s) >> 3;
+                            xf[c][u][s] =
+                                *(const uint4 *)(cur + (32 * c + r) * 128 + ((chunk ^ swz) << 4));
+                        }
+                // Group g = (u * S + s) * A + a is one 32-row x 16-k MFMA operand
+                // and its C MFMAs. 4-bit: group 0 is dequantized here, under the
+                // latency of the x reads, and every later group in slices between
+                // the MFMAs of the group before it (below). 8-bit keeps one
+                // dequant per group ahead of its MFMAs: its dequant is lighter,
+                // and the pipeline's extra live registers made the 128-token dual
+                // tile spill (M = 2048: 335 -> 395 us).
+                constexpr bool PIPED = BITS == 4;
+                typedef Dequant8<T, BITS> Dq;
+                auto dq_init = [&](Dq &d, int g) {
+                    const int u = g / (S * A), s = (g / A) % S, a = g % A;
+                    const uint32_t words[4] = {wq[a][u].x, wq[a][u].y, wq[a][u].z, wq[a][u].w};
+                    d.init(BITS == 4 ? words[s] : words[2 * s], BITS == 4 ? 0u : words[2 * s + 1],
+                           (float)__builtin_bit_cast(T, (uint16_t)sq[a][u]),
+                           (float)__builtin_bit_cast(T, (uint16_t)bq[a][u]));
+                };
+                uint32_t opa[4];  // the next MFMA operand: four packed pairs
+                if constexpr (PIPED) {
+                    Dq d;
+                    dq_init(d, 0);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        opa[k] = d.pair(k);
+                        launder(opa[k]);  // computed here, not sunk to its MFMA
+                    }
+                }
+                const int nx = st + 1 < last ? st + 1 : last;
+                // the slot's reads have returned before its refill is issued
+                __builtin_amdgcn_sched_barrier(0);
+                wait_lgkmcnt0();
+                issue(nx, slot);
+                if constexpr (Sh::WREG) {  // one stage ahead, into the other set
+                    load_w(nx, wreg[(j + 1) % 2]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                // Software pipeline: each MFMA of group g is followed by a slice
+                // of group g + 1's dequant (pair k after MFMA k * C / 4), so one
+                // wave issues its VALU while its MFMAs run. The laundered pairs
+                // and the fences keep instruction selection and the scheduler
+                // from clustering the MFMAs again (they did, four at a time,
+                // leaving the dequant exposed). Each accumulator still receives
+                // its MFMAs in K order: the results do not change.
+                constexpr int NG = SPS * S * A;
+#pragma unroll
+                for (int g = 0; g < NG; ++g) {
+                    const int u = g / (S * A), s = (g / A) % S, a = g % A;
+                    Dq d;
+                    if constexpr (!PIPED) {
+                        dq_init(d, g);
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) opa[k] = d.pair(k);
+                    }
+                    const V8 af = __builtin_bit_cast(V8, (uint4){opa[0], opa[1], opa[2], opa[3]});
+                    if constexpr (!PIPED) {
+#pragma unroll
+                        for (int c = 0; c < C; ++c)
+                            acc[a][c] = Mfma<T>::mma(af, __builtin_bit_cast(V8, xf[c][u][s]), acc[a][c]);
+                        continue;
+                    }
+#pragma unroll
+                    for (int c = 0; c < C; ++c) {
+                        acc[a][c] = Mfma<T>::mma(af, __builtin_bit_cast(V8, xf[c][u][s]), acc[a][c]);
+                        if (g + 1 < NG) {
+                            if (c == 0) {
+                                dq_init(d, g + 1);
+                                launder(d.a);
+                                launder(d.b);
+                            }
+#pragma unroll
+                            for (int k = 0; k < 4; ++k)
+                                if ((k * C) / 4 == c) {
+                                    opa[k] = d.pair(k);
+                                    launder(opa[k]);
+                                }
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+                load_sb(st < last ? st + 1 : last);
             }
+        }
+        };
+        mainloop(xbuf, sbt);
+        // the loads issued past the last stage land before the LDS is reused for
+        // the reduction or released with the workgroup
+        wait_vmcnt<0>();
+
+        if constexpr (Sh::KG > 1) {
+            // Fixed-order reduction of the K-split partial tiles: K-group 0 adds
+            // groups 1, 2, ... in turn. The ring's LDS is reused, RSLOTS partials
+            // per round, so every wave must be done with its x stages first; all
+            // waves take part in every round's barriers.
+            constexpr int REGS = A * C * 16;
+            float *red = (float *)lds;
             __syncthreads();
-            if (kw == 0) {
-                for (int src = r0; src < r1; ++src) {
-                    const float *sp = red + (size_t)(src - r0) * REGS * 64 + lane;
+            for (int r0 = 1; r0 < wk; r0 += Sh::RSLOTS) {  // workgroup-uniform
+                const int r1 = r0 + Sh::RSLOTS < wk ? r0 + Sh::RSLOTS : wk;
+                if (kw >= r0 && kw < r1) {
+                    float *dst = red + (size_t)(kw - r0) * REGS * 64 + lane;
 #pragma unroll
                     for (int a = 0; a < A; ++a)
 #pragma unroll
                         for (int c = 0; c < C; ++c)
 #pragma unroll
-                            for (int i = 0; i < 16; ++i) acc[a][c][i] += sp[((a * C + c) * 16 + i) * 64];
+                            for (int i = 0; i < 16; ++i) dst[((a * C + c) * 16 + i) * 64] = acc[a][c][i];
                 }
+                __syncthreads();
+                if (kw == 0) {
+                    for (int src = r0; src < r1; ++src) {
+                        const float *sp = red + (size_t)(src - r0) * REGS * 64 + lane;
+#pragma unroll
+                        for (int a = 0; a < A; ++a)
+#pragma unroll
+                            for (int c = 0; c < C; ++c)
+#pragma unroll
+                                for (int i = 0; i < 16; ++i) acc[a][c][i] += sp[((a * C + c) * 16 + i) * 64];
+                    }
+                }
+                if (r1 < wk) __syncthreads();  // the slots are refilled next round
             }
-            if (r1 < wk) __syncthreads();  // the slots are refilled next round
         }
-        if (kw > 0) return;
+        if constexpr (KM == KM_LOOP) {
+            // wave 0 folds the part into the running sums, in part order; the
+            // barrier keeps the next part's DMAs off the slots until it has read
+            // the other waves' partials
+            if (kw == 0) {
+#pragma unroll
+                for (int a = 0; a < A; ++a)
+#pragma unroll
+                    for (int c = 0; c < C; ++c)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) {
+                            float *sp = psum + ((a * C + c) * 16 + i) * 64 + lane;
+                            *sp = kp == 0 ? acc[a][c][i] : *sp + acc[a][c][i];
+                        }
+            }
+            __syncthreads();
+        }
+    }  // K parts
+    if (kw > 0) return;
+    if constexpr (KM == KM_LOOP) {
+#pragma unroll
+        for (int a = 0; a < A; ++a)
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[a][c][i] = psum[((a * C + c) * 16 + i) * 64 + lane];
+    }
+    if constexpr (KM == KM_PART) {
+        // one K part's sums, fp32 [ks, M, Nout] (single-part epilogues; the
+        // host checks Nout % 4 == 0): a second kernel adds the parts
+        float *dst = p.part + (int64_t)kz * p.M * bd.Nout;
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            const int64_t m = m_blk + 32 * c + r;
+#pragma unroll
+            for (int a = 0; a < A; ++a)
+#pragma unroll
+                for (int blk = 0; blk < 4; ++blk) {
+                    const int64_t n = n_wave + 32 * a + 8 * blk + 4 * h;
+                    if (m < p.M && n < bd.Nout)
+                        *(float4 *)(dst + m * bd.Nout + n) =
+                            make_float4(acc[a][c][4 * blk], acc[a][c][4 * blk + 1],
+                                        acc[a][c][4 * blk + 2], acc[a][c][4 * blk + 3]);
+                }
+        }
+        return;
     }
 
     // D[row][col] of a 32x32 tile: col = lane % 32 (token), row = 8*(i/4) +
@@ -983,14 +1062,14 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
-template <typename T, int BITS, int A, int C, int WK, int EPI>
+template <typename T, int BITS, int A, int C, int WK, int EPI, int KM>
 __global__ __launch_bounds__(64 * WK)
 __attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<A, C>()))) void qmm_mfma_kernel(
     QParams p) {
     constexpr int TN = (epi_parts(EPI) == 1) ? A : 1;
     __shared__ __attribute__((aligned(16))) char lds[MfmaShape<T, BITS, A, C, WK>::LDS];
-    qmm_mfma_tile<T, BITS, A, C, WK, EPI>(p, lds, (int64_t)blockIdx.x * (32 * TN),
-                                          (int64_t)blockIdx.y * (32 * C));
+    qmm_mfma_tile<T, BITS, A, C, WK, EPI, KM>(p, lds, (int64_t)blockIdx.x * (32 * TN),
+                                              (int64_t)blockIdx.y * (32 * C), (int)blockIdx.z);
 }
 
 // Block i of a run of n feature tiles that take g workgroups each (the g
@@ -1072,27 +1151,45 @@ int launch_qmv(const QParams &p, hipStream_t st) {
     return launch_status("quantized matmul (qmv)");
 }
 
-// LDS of one workgroup: the static stage rings plus the waves' scale/bias
-// tables (dynamic).
-template <typename T, int BITS, int A, int C>
-int64_t mfma_lds_bytes(const QParams &p, int wk) {
-    const SbtLayout tl = sbt_layout(p.K / wk, p.gs);
-    return MfmaShape<T, BITS, A, C, 4>::LDS + (int64_t)wk * A * 2 * tl.array_bytes;
+// k values of the longest of the ks * wk wave chunks of K
+inline int kslice_of(int64_t K, int ks, int wk) {
+    return (int)ceil_div(K / XK, (int64_t)ks * wk) * XK;
 }
 
-template <typename T, int BITS, int A, int C, int EPI>
+// Running sums over the K parts (a workgroup that runs them in turn): one
+// fp32 per accumulator register and lane.
+inline int64_t mfma_sum_bytes(const QParams &p, int A, int C) {
+    return (p.ks > 1 && !p.part) ? (int64_t)A * C * 16 * 64 * 4 : 0;
+}
+
+// Dynamic LDS of one workgroup: the waves' scale/bias tables and the sums
+// over the K parts.
+inline int64_t mfma_dyn_bytes(const QParams &p, int A, int C, int wk) {
+    const SbtLayout tl = sbt_layout(kslice_of(p.K, p.ks, wk), p.gs);
+    return (int64_t)wk * A * 2 * tl.array_bytes + mfma_sum_bytes(p, A, C);
+}
+
+// LDS of one workgroup: the static stage slots plus the dynamic part.
+template <typename T, int BITS, int A, int C>
+int64_t mfma_lds_bytes(const QParams &p, int wk) {
+    return MfmaShape<T, BITS, A, C, 4>::LDS + mfma_dyn_bytes(p, A, C, wk);
+}
+
+// p.ks K parts in grid z when p.part is set, else each workgroup runs them.
+template <typename T, int BITS, int A, int C, int EPI, int KM = KM_ONE>
 int launch_mfma_cfg(QParams p, int wk, hipStream_t st) {
     constexpr int P = epi_parts(EPI);
     constexpr int TN = (P == 1) ? A : 1;
     p.wk = wk;
-    const SbtLayout tl = sbt_layout(p.K / wk, p.gs);
-    p.sbp = tl.pitch;
-    const size_t dyn = (size_t)wk * A * 2 * tl.array_bytes;
+    p.kslice = kslice_of(p.K, p.ks, wk);
+    p.sbp = sbt_layout(p.kslice, p.gs).pitch;
+    const size_t dyn = (size_t)mfma_dyn_bytes(p, A, C, wk);
     if (mfma_lds_bytes<T, BITS, A, C>(p, wk) > LDS_PER_CU)
         return fail(MI_ERR_UNSUPPORTED, "quantized matmul tile exceeds the LDS (K = %lld)",
                     (long long)p.K);
-    const dim3 grid((unsigned)ceil_div(p.Nout, 32 * TN), (unsigned)ceil_div(p.M, 32 * C));
-    qmm_mfma_kernel<T, BITS, A, C, 4, EPI><<<grid, 64 * wk, dyn, st>>>(p);
+    const dim3 grid((unsigned)ceil_div(p.Nout, 32 * TN), (unsigned)ceil_div(p.M, 32 * C),
+                    p.part ? (unsigned)p.ks : 1u);
+    qmm_mfma_kernel<T, BITS, A, C, 4, EPI, KM><<<grid, 64 * wk, dyn, st>>>(p);
     return launch_status("quantized matmul (mfma)");
 }
 
@@ -1116,10 +1213,10 @@ int device_cus() {
 template <typename T, int BITS, int A, int EPI, int CB>
 int launch_mfma_mixed(QParams p, int nb, int64_t nt, hipStream_t st) {
     p.wk = 4;
-    const SbtLayout tl = sbt_layout(p.K / 4, p.gs);
-    p.sbp = tl.pitch;
+    p.kslice = kslice_of(p.K, p.ks, 4);
+    p.sbp = sbt_layout(p.kslice, p.gs).pitch;
     p.n4 = nb;
-    const size_t dyn = (size_t)4 * A * 2 * tl.array_bytes;
+    const size_t dyn = (size_t)mfma_dyn_bytes(p, A, CB, 4);
     const unsigned blocks = (unsigned)(nb * (4 / CB) + (nt - nb) * (8 / CB));
     qmm_mfma_mixed_kernel<T, BITS, A, EPI, CB><<<blocks, 256, dyn, st>>>(p);
     return launch_status("quantized matmul (mfma, mixed tiles)");
@@ -1143,6 +1240,14 @@ int launch_mfma(const QParams &p, hipStream_t st) {
     constexpr int P = epi_parts(EPI);
     const int64_t stages = p.K / XK;
     const int wk = (stages % 4 == 0) ? 4 : (stages % 2 == 0 ? 2 : 1);
+    // Several K parts without a workspace: each workgroup runs them in turn,
+    // on 32-token tiles (the _ws entries run them as workgroups of their own)
+    if (p.ks > 1) {
+        if (mfma_lds_bytes<T, BITS, P, 1>(p, wk) <= LDS_PER_CU)
+            return launch_mfma_cfg<T, BITS, P, 1, EPI, KM_LOOP>(p, wk, st);
+        return fail(MI_ERR_UNSUPPORTED, "quantized matmul tile exceeds the LDS (K = %lld)",
+                    (long long)p.K);
+    }
     const int64_t nt = ceil_div(p.Nout, 32);
     const bool large = p.M >= 512 || nt * ceil_div(p.M, 64) > 2048;
     if constexpr (P == 1) {
@@ -1213,22 +1318,71 @@ int launch_qmv_dot2(const QParams &p, int mr, hipStream_t st) {
     return launch_status("quantized matmul (dot2 qmv)");
 }
 
+// Shapes the MFMA kernel takes (16-bit T): it addresses x and each weight
+// array with 32-bit offsets and copies scale/bias pairs with 4-byte loads (an
+// even group count). wrows: rows of the largest part's arrays.
+inline bool mfma_shape_ok(int64_t M, int64_t K, int64_t wrows, int gs, int bits) {
+    return M > QMV_MR && K % XK == 0 && (K / gs) % 2 == 0 && M * K < ((int64_t)1 << 31) &&
+           wrows * K * bits / 8 < ((int64_t)1 << 32);
+}
+
 template <typename T, int EPI>
 int launch_typed(const QParams &p, int bits, hipStream_t st) {
-    // the MFMA kernel addresses x and each weight array with 32-bit offsets
-    const int64_t wrows = p.noff[2] + p.Nout;  // rows of the largest part's arrays
-    // and copies scale/bias pairs with 4-byte loads (an even group count)
-    const bool mfma = (sizeof(T) == 2) && p.M > QMV_MR && (p.K % XK == 0) &&
-                      (p.K / p.gs) % 2 == 0 && p.M * p.K < ((int64_t)1 << 31) &&
-                      wrows * p.K * bits / 8 < ((int64_t)1 << 32);
+    const bool mfma = (sizeof(T) == 2) && mfma_shape_ok(p.M, p.K, p.noff[2] + p.Nout, p.gs, bits);
     if constexpr (sizeof(T) == 2) {
         const int mr = p.M == 1 ? 1 : (p.M == 2 ? 2 : 4);
         if (bits == 4 && p.M <= 4 && qmv_dot2_lds_bytes(mr, p.K) <= 65536)
             return launch_qmv_dot2<T, EPI>(p, mr, st);
-        if (mfma)
-            return bits == 4 ? launch_mfma<T, 4, EPI>(p, st) : launch_mfma<T, 8, EPI>(p, st);
+        if (mfma) {
+            QParams q = p;
+            q.ks = kpart_count(p.M, p.K);
+            q.part = nullptr;
+            return bits == 4 ? launch_mfma<T, 4, EPI>(q, st) : launch_mfma<T, 8, EPI>(q, st);
+        }
     }
     return bits == 4 ? launch_qmv<T, 4, EPI>(p, st) : launch_qmv<T, 8, EPI>(p, st);
+}
+
+// The K-part launch (p.part set): 128-token tiles when M > 64, so a part
+// dequantizes each weight once, and 64-feature tiles (4-bit) while they still
+// make 128 workgroups. Single-part epilogues only; the parts kernel stores
+// sums, and the epilogue runs in the kernel that adds them.
+template <typename T, int BITS>
+int launch_parts(const QParams &p, hipStream_t st) {
+    const int64_t stages = p.K / XK;
+    const int wk = (stages % 4 == 0) ? 4 : (stages % 2 == 0 ? 2 : 1);
+    const int C = p.M > 64 ? 4 : (p.M > 32 ? 2 : 1);
+    const bool a2 = ceil_div(p.Nout, 64) * ceil_div(p.M, 32 * C) * p.ks >= 128;
+    if constexpr (BITS == 4) {  // (the 8-bit 64x128 tile spills)
+        if (a2 && C == 4 && mfma_lds_bytes<T, BITS, 2, 4>(p, wk) <= LDS_PER_CU)
+            return launch_mfma_cfg<T, BITS, 2, 4, EPI_STORE, KM_PART>(p, wk, st);
+        if (a2 && C == 2) return launch_mfma_cfg<T, BITS, 2, 2, EPI_STORE, KM_PART>(p, wk, st);
+    }
+    if (C == 4) return launch_mfma_cfg<T, BITS, 1, 4, EPI_STORE, KM_PART>(p, wk, st);
+    if (C == 2) return launch_mfma_cfg<T, BITS, 1, 2, EPI_STORE, KM_PART>(p, wk, st);
+    return launch_mfma_cfg<T, BITS, 1, 1, EPI_STORE, KM_PART>(p, wk, st);
+}
+
+// Adds the K parts of p.part in part order and applies the single-part
+// epilogue EPI; thread t owns outputs 4t .. 4t + 3 (Nout % 4 == 0).
+template <typename T, int EPI>
+__global__ __launch_bounds__(256) void qmm_parts_sum_kernel(QParams p) {
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t size = p.M * p.Nout;
+    if (4 * q >= size) return;
+    const int64_t o = 4 * q, m = o / p.Nout, n = o - m * p.Nout;
+    float4 v = *(const float4 *)(p.part + o);
+    float s[1][4] = {{v.x, v.y, v.z, v.w}};
+    for (int z = 1; z < p.ks; ++z) {
+        v = *(const float4 *)(p.part + z * size + o);
+        s[0][0] += v.x;
+        s[0][1] += v.y;
+        s[0][2] += v.z;
+        s[0][3] += v.w;
+    }
+    int64_t nb = 0;
+    const Bound bd = bind<EPI>(p, nb);
+    epi4<T, EPI, 1>(p, bd, m, n, s);
 }
 
 template <int EPI>
@@ -1259,6 +1413,7 @@ QParams base_params(const void *x, const uint32_t *w, const void *s, const void 
     p.gs = gs;
     p.gs_log2 = ilog2(gs);
     p.wk = 1;
+    p.ks = 1;
     return p;
 }
 
@@ -1285,6 +1440,53 @@ int qmm_residual_launch(const void *x, const uint32_t *w, const void *s, const v
     return run<EPI_RESID>(p, bits, dtype, stream);
 }
 
+int64_t qmm_parts_bytes(int64_t M, int64_t N, int64_t K, int gs, int bits, int dtype) {
+    if (dtype != MI_BF16 && dtype != MI_F16) return 0;
+    if ((bits != 4 && bits != 8) || (gs != 32 && gs != 64 && gs != 128) || M < 0 || N <= 0)
+        return 0;
+    const int ks = kpart_count(M, K);
+    if (ks < 2 || N % 4 || !mfma_shape_ok(M, K, N, gs, bits)) return 0;
+    return (int64_t)ks * M * N * (int64_t)sizeof(float);
+}
+
+int qmm_parts_launch(const void *x, const uint32_t *w, const void *s, const void *b, float *part,
+                     int64_t M, int64_t N, int64_t K, int gs, int bits, int dtype, void *stream) {
+    if (int e = check_common(x, w, s, b, part, M, N, K, gs, bits, dtype)) return e;
+    QParams p = base_params(x, w, s, b, nullptr, M, N, K, gs);
+    p.ks = kpart_count(M, K);
+    p.part = part;
+    hipStream_t st = as_stream(stream);
+    if (dtype == MI_BF16)
+        return bits == 4 ? launch_parts<bf16, 4>(p, st) : launch_parts<bf16, 8>(p, st);
+    return bits == 4 ? launch_parts<f16, 4>(p, st) : launch_parts<f16, 8>(p, st);
+}
+
+namespace {
+
+// The workspace entries: the K parts as workgroups of their own, then their
+// sum with the epilogue; the one-launch path (same sums, same order) when the
+// shape has one K part or the workspace is missing or short.
+template <int EPI>
+int run_ws(QParams p, int bits, int dtype, void *ws, int64_t ws_bytes, void *stream) {
+    if (p.M == 0 || p.Nout == 0) return MI_OK;
+    const int64_t need = qmm_parts_bytes(p.M, p.Nout, p.K, p.gs, bits, dtype);
+    if (need == 0 || !ws || ws_bytes < need || !aligned(ws, 16))
+        return run<EPI>(p, bits, dtype, stream);
+    if (int e = qmm_parts_launch(p.x, p.w[0], p.s[0], p.b[0], (float *)ws, p.M, p.Nout, p.K, p.gs,
+                                 bits, dtype, stream))
+        return e;
+    p.ks = kpart_count(p.M, p.K);
+    p.part = (float *)ws;
+    const unsigned blocks = (unsigned)ceil_div(p.M * p.Nout / 4, 256);
+    if (dtype == MI_BF16)
+        qmm_parts_sum_kernel<bf16, EPI><<<blocks, 256, 0, as_stream(stream)>>>(p);
+    else
+        qmm_parts_sum_kernel<f16, EPI><<<blocks, 256, 0, as_stream(stream)>>>(p);
+    return launch_status("quantized matmul (sum of K parts)");
+}
+
+}  // namespace
+
 }  // namespace mi
 
 using namespace mi;
@@ -1303,6 +1505,33 @@ extern "C" int mi_qmm_affine_residual(const void *x, const uint32_t *w, const vo
                                       void *stream) {
     return qmm_residual_launch(x, w, scales, biases, resid, y, M, N, K, group_size, bits, dtype,
                                stream);
+}
+
+extern "C" int64_t mi_qmm_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size,
+                                          int bits, int dtype) {
+    return qmm_parts_bytes(M, N, K, group_size, bits, dtype);
+}
+
+extern "C" int mi_qmm_affine_ws(const void *x, const uint32_t *w, const void *scales,
+                                const void *biases, void *y, int64_t M, int64_t N, int64_t K,
+                                int group_size, int bits, int dtype, void *workspace,
+                                int64_t workspace_bytes, void *stream) {
+    if (int e = check_common(x, w, scales, biases, y, M, N, K, group_size, bits, dtype)) return e;
+    return run_ws<EPI_STORE>(base_params(x, w, scales, biases, y, M, N, K, group_size), bits,
+                             dtype, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mi_qmm_affine_residual_ws(const void *x, const uint32_t *w, const void *scales,
+                                         const void *biases, const void *resid, void *y,
+                                         int64_t M, int64_t N, int64_t K, int group_size,
+                                         int bits, int dtype, void *workspace,
+                                         int64_t workspace_bytes, void *stream) {
+    if (int e = check_common(x, w, scales, biases, y, M, N, K, group_size, bits, dtype)) return e;
+    if (M && N && !resid) return fail(MI_ERR_ARG, "null residual");
+    if (!aligned(resid, 8)) return fail(MI_ERR_ARG, "residual must be 8-byte aligned");
+    QParams p = base_params(x, w, scales, biases, y, M, N, K, group_size);
+    p.resid = resid;
+    return run_ws<EPI_RESID>(p, bits, dtype, workspace, workspace_bytes, stream);
 }
 
 extern "C" int mi_qmm_affine_split_gate(const void *x, const uint32_t *w, const void *scales,

@@ -211,6 +211,117 @@ def test_qmm_residual_rmsnorm(M):
     _close(y, oracle.rms_norm(to_np(h), nw, 1e-5, "bfloat16"), "bfloat16")
 
 
+# ----------------------------------------------------------------- K parts
+
+
+def _kparts_call(name, *args):
+    st = torch.cuda.current_stream().cuda_stream
+    status = getattr(hip.lib(), name)(*args, st)
+    assert status == 0, hip.lib().mi_last_error()
+
+
+@pytest.mark.parametrize("M,N,K,bits,dtype", [
+    (128, 2560, 4096, 4, "bfloat16"),   # o_proj: 2 K parts
+    (128, 2560, 9728, 4, "bfloat16"),   # down_proj: 4 parts of 9 or 10 stages
+    (100, 200, 4096, 8, "bfloat16"),    # ragged M and N, 8-bit
+    (40, 512, 8192, 4, "float16"),      # 64-token part tiles
+    (16, 256, 4224, 4, "bfloat16"),     # 66 stages, two waves a part: chunks of 16 / 17
+])
+def test_qmm_k_parts_workspace_equals_one_launch(M, N, K, bits, dtype):
+    """At shapes with K parts the _ws entries (the parts as workgroups of their
+    own, then a kernel that adds them) equal, bit for bit, the entries without
+    a workspace (each workgroup runs the parts in turn), for [qmm], [qmm, add]
+    and [qmm, add, rms_norm]; and both are within tolerance of the oracle. A
+    workspace one byte short takes the one-launch path, same bits."""
+    L = hip.lib()
+    r = rng(900 + M + K)
+    dt = hip._DT[getattr(torch, dtype)]
+    x = oracle.round_to(r.normal(0, 1, (M, K)), dtype)
+    res = oracle.round_to(r.normal(0, 1, (M, N)), dtype)
+    nw = oracle.round_to(1 + 0.1 * r.normal(0, 1, N), dtype)
+    q = _quant(901, N, K, 64, bits, dtype)
+    xd, rd, nwd = to_torch(x, dtype), to_torch(res, dtype), to_torch(nw, dtype)
+    w, s, b = _dev(*q, dtype)
+    nbytes = L.mi_qmm_workspace_bytes(M, N, K, 64, bits, dt)
+    parts = 2 if K < 8192 else 4
+    assert nbytes == parts * M * N * 4
+    ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device="cuda")  # NaN partials
+    P = hip._ptr
+    ys = {}
+    for mode, (wsp, wsb) in (("one", (None, 0)), ("ws", (P(ws), nbytes)),
+                             ("short", (P(ws), nbytes - 1))):
+        y = torch.empty(M, N, dtype=xd.dtype, device="cuda")
+        yr = torch.empty_like(y)
+        h, yn = torch.empty_like(y), torch.empty_like(y)
+        if mode == "one":
+            _kparts_call("mi_qmm_affine", P(xd), P(w), P(s), P(b), P(y), M, N, K, 64, bits, dt)
+            _kparts_call("mi_qmm_affine_residual", P(xd), P(w), P(s), P(b), P(rd), P(yr), M, N, K,
+                         64, bits, dt)
+            _kparts_call("mi_qmm_affine_residual_rmsnorm", P(xd), P(w), P(s), P(b), P(rd), P(nwd),
+                         1e-6, P(h), P(yn), M, N, K, 64, bits, dt)
+        else:
+            _kparts_call("mi_qmm_affine_ws", P(xd), P(w), P(s), P(b), P(y), M, N, K, 64, bits, dt,
+                         wsp, wsb)
+            _kparts_call("mi_qmm_affine_residual_ws", P(xd), P(w), P(s), P(b), P(rd), P(yr), M, N,
+                         K, 64, bits, dt, wsp, wsb)
+            _kparts_call("mi_qmm_affine_residual_rmsnorm_ws", P(xd), P(w), P(s), P(b), P(rd),
+                         P(nwd), 1e-6, P(h), P(yn), M, N, K, 64, bits, dt, wsp, wsb)
+        torch.cuda.synchronize()
+        ys[mode] = (y, yr, h, yn)
+    for mode in ("ws", "short"):
+        for a, c, what in zip(ys["one"], ys[mode], ("qmm", "qmm+add", "h", "rms_norm(h)")):
+            assert torch.equal(a, c), f"{mode}: {what} differs from the one-launch entry"
+    y, yr, h, yn = ys["ws"]
+    want = oracle.quantized_matmul(x, *q, 64, bits, dtype)
+    _close(y, want, dtype)
+    _close(yr, oracle.round_to(res.astype(np.float64) + want, dtype), dtype)
+    assert torch.equal(yr, h)
+    _close(yn, oracle.rms_norm(to_np(h), nw, 1e-6, dtype), dtype)
+    # the ops layer takes the workspace path: same bits
+    assert torch.equal(ops.quantized_matmul(xd, w, s, b, group_size=64, bits=bits), y)
+
+
+def test_qmm_k_parts_workspace_size():
+    """The split rule is a function of (M, K): 8 < M <= 128 and K >= 4096 on
+    the 16-bit MFMA path; N must be a multiple of 4."""
+    L = hip.lib()
+    bf = hip._DT[torch.bfloat16]
+    assert L.mi_qmm_workspace_bytes(128, 2560, 4096, 64, 4, bf) == 2 * 128 * 2560 * 4
+    assert L.mi_qmm_workspace_bytes(128, 2560, 9728, 64, 4, bf) == 4 * 128 * 2560 * 4
+    assert L.mi_qmm_workspace_bytes(9, 64, 8192, 64, 8, bf) == 4 * 9 * 64 * 4
+    for M, N, K, dt in ((8, 2560, 4096, bf), (129, 2560, 4096, bf), (128, 9728, 2560, bf),
+                        (128, 2562, 4096, bf), (128, 2560, 4096, hip._DT[torch.float32])):
+        assert L.mi_qmm_workspace_bytes(M, N, K, 64, 4, dt) == 0
+
+
+@pytest.mark.parametrize("M", [100, 128])
+def test_k_parts_multi_part_epilogues_equal_their_op_streams(M):
+    """Dual, SwiGLU, split(3) and grouped q/k/v at K = 4096 run the parts in
+    turn inside one launch; each equals, bit for bit, the op stream built from
+    single-part quantized matmuls (which take the workspace path)."""
+    r = rng(950 + M)
+    K = 4096
+    x = oracle.round_to(r.normal(0, 1, (1, M, K)), "bfloat16")
+    xd = to_torch(x, "bfloat16")
+    q1, q3 = _quant(951, 256, K), _quant(952, 256, K)
+    w1, w3 = _dev(*q1, "bfloat16"), _dev(*q3, "bfloat16")
+    g, u = ops.qmm_dual(xd, *w1, *w3)
+    assert torch.equal(g, ops.quantized_matmul(xd, *w1))
+    assert torch.equal(u, ops.quantized_matmul(xd, *w3))
+    assert torch.equal(ops.qmm_dual(xd, *w1, *w3, swiglu=True), ops.swiglu(g, u))
+    _close(g, oracle.quantized_matmul(x, *q1, 64, 4, "bfloat16"), "bfloat16")
+    q = _quant(953, 3 * 128, K)
+    wq = _dev(*q, "bfloat16")
+    c, bx = ops.qmm_split_gate(xd, *wq)
+    full = ops.quantized_matmul(xd, *wq)
+    assert torch.equal(c, full[..., 128:256])
+    assert torch.equal(bx, (full[..., :128].float() * full[..., 256:].float()).to(torch.bfloat16))
+    qs = [_quant(954 + i, n, K) for i, n in enumerate((256, 64, 96))]
+    wg = [_dev(*qq, "bfloat16") for qq in qs]
+    for y, ww in zip(ops.qmm_grouped3(xd, wg), wg):
+        assert torch.equal(y, ops.quantized_matmul(xd, *ww))
+
+
 @pytest.mark.parametrize("M", [1, 100, 300])
 def test_qmm_split_gate(M):
     r = rng(600 + M)

@@ -120,9 +120,11 @@ def test_split_gate_region(M, D, K):
     _gates(regions.split_gate(), [to_torch(x, BF)] + _dev(q), [c_o, (bx, None)])
 
 
-@pytest.mark.parametrize("M,N,K", [(100, 200, 512), (128, 2560, 4096), (7, 200, 512)])
+@pytest.mark.parametrize("M,N,K", [(100, 200, 512), (128, 2560, 4096), (128, 2560, 9728),
+                                   (7, 200, 512)])
 def test_residual_regions(M, N, K):
-    """[qmm, add] and [qmm, add, rms_norm] (o_proj / down_proj shapes)."""
+    """[qmm, add] and [qmm, add, rms_norm] (o_proj / down_proj shapes: K parts
+    run as workgroups of their own, then a kernel adds them)."""
     q = _quant(2040, N, K)
     x = _x(2041 + M, (1, M, K))
     res = _x(2042 + M, (1, M, N))
