@@ -107,6 +107,9 @@ class SizedRegions(ReplayWrapper):
         spec = self._specs.get(role)
         if spec is None:
             return None
+        return self._try_spec(spec, inputs, n)
+
+    def _try_spec(self, spec, inputs, n: int):
         ranges = self.__dict__.get("_ranges", type(self).RANGES)
         if ranges is not None and not in_runs(n, ranges.get(spec.kernel_id, ())):
             return None

@@ -19,6 +19,12 @@ fallback predicate fires (patch/wrappers.py:51-55 pattern):
   [qmm(down), add]                                       -> residual
   reshape -> q_norm/k_norm -> transpose -> rope (+cache)  -> norm_rope
 
+``install_regions`` also links neighbouring layers: layer i's last cut
+becomes [qmm(down), add, rms_norm(layer i+1's input_layernorm)], the same
+region kind as the o_proj cut, and layer i+1 takes that normalized output
+instead of normalizing its input again (one launch fewer per layer, same
+bits).
+
 Only the last position's logits are computed in prefill (the caller takes
 logits[:, -1] before sampling; everything before it is dead work,
 docs/measurement.md:74-83).
@@ -191,6 +197,26 @@ def layer_specs(cfg: Qwen3Config, dtype: str = "bfloat16") -> dict:
     }
 
 
+class NormHandoff:
+    """The next layer's normalized input, made by the previous layer's last
+    region together with that layer's output h. It is handed over only for
+    that very tensor: a layer called with any other input normalizes it
+    itself."""
+
+    __slots__ = ("h", "hn")
+
+    def __init__(self):
+        self.h = self.hn = None
+
+    def put(self, h, hn) -> None:
+        self.h, self.hn = h, hn
+
+    def take(self, x):
+        h, hn = self.h, self.hn
+        self.h = self.hn = None
+        return hn if h is x else None
+
+
 class Qwen3LayerRegions(SizedRegions):
     """The decoder layer with the region cuts spliced in (try_sized at the
     sizes each kernel serves, else the original ops). A spec missing from the
@@ -199,6 +225,13 @@ class Qwen3LayerRegions(SizedRegions):
     KERNEL_IDS = ["qwen3_qkv_proj", "qwen3_o_proj_add_norm", "qwen3_gate_up_swiglu",
                   "qwen3_down_add"]
 
+    def link(self, prev: NormHandoff | None = None, nxt=None) -> None:
+        """prev: where the previous layer leaves this layer's normalized input;
+        nxt: (the next layer's input RMSNorm, the [qmm(down), add, rms_norm]
+        spec, the handoff to the next layer). Plain attributes, not submodules."""
+        self.__dict__["_prev"] = prev
+        self.__dict__["_next"] = nxt
+
     def forward(self, x, cache: KVCache):
         w = self.wrapped
         if not (x.dim() == 3 and x.dtype == torch.bfloat16 and x.is_cuda):
@@ -206,7 +239,10 @@ class Qwen3LayerRegions(SizedRegions):
         attn, mlp = w.self_attn, w.mlp
         c = attn.cfg
         B, L, _ = x.shape
-        xn = w.input_layernorm(x)
+        prev = self.__dict__.get("_prev")
+        xn = prev.take(x) if prev is not None else None
+        if xn is None:
+            xn = w.input_layernorm(x)
         projs = (attn.q_proj, attn.k_proj, attn.v_proj)
         outs = self._try("qkv", [xn] + [t for m in projs for t in (m.weight, m.scales, m.biases)],
                          L)
@@ -232,15 +268,34 @@ class Qwen3LayerRegions(SizedRegions):
                          [hn, g.weight, g.scales, g.biases, u.weight, u.scales, u.biases], L)
         act = ops.swiglu(g(hn), u(hn)) if outs is None else outs[0]
         d = mlp.down_proj
+        nxt = self.__dict__.get("_next")
+        if nxt is not None:
+            norm, spec, handoff = nxt
+            outs = self._try_spec(spec, [act, d.weight, d.scales, d.biases, h, norm.weight], L)
+            if outs is not None:
+                handoff.put(outs[0], outs[1])
+                return outs[0]
         outs = self._try("residual", [act, d.weight, d.scales, d.biases, h], L)
         return h + d(act) if outs is None else outs[0]
 
 
-def install_regions(model: Qwen3Model) -> list:
-    """Swap the region wrapper in at every model.layers.i; returns the occupants."""
-    specs = layer_specs(model.cfg)
-    return [install(model, f"model.layers.{i}", Qwen3LayerRegions(layer, specs))
-            for i, layer in enumerate(model.model.layers)]
+def install_regions(model: Qwen3Model, link_layers: bool = True) -> list:
+    """Swap the region wrapper in at every model.layers.i; returns the
+    occupants. link_layers: each layer's down_proj cut also normalizes the
+    next layer's input (NormHandoff)."""
+    cfg = model.cfg
+    specs = layer_specs(cfg)
+    layers = list(model.model.layers)
+    wrappers = [Qwen3LayerRegions(layer, specs) for layer in layers]
+    if link_layers:
+        spec = regions.residual_rmsnorm("qwen3_down_add_next_norm", "bfloat16", cfg.group_size,
+                                        cfg.bits, cfg.rms_norm_eps)
+        for i in range(len(layers) - 1):
+            handoff = NormHandoff()
+            wrappers[i].link(prev=wrappers[i].__dict__.get("_prev"),
+                             nxt=(layers[i + 1].input_layernorm, spec, handoff))
+            wrappers[i + 1].link(prev=handoff)
+    return [install(model, f"model.layers.{i}", wr) for i, wr in enumerate(wrappers)]
 
 
 # ---------------------------------------------------------------------------

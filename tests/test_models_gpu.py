@@ -95,6 +95,44 @@ def test_qwen3_layer_config3(L, offset):
 
 
 @pytest.mark.gpu
+def test_qwen3_linked_layers_equal_unlinked_and_original():
+    """install_regions links neighbouring layers: layer i's down_proj cut also
+    normalizes layer i+1's input (NormHandoff). A 3-layer model's prefill
+    (K parts at M = 128) and decode step (M = 1) give the original ops'
+    logits bit for bit with and without the links, and every link is used."""
+    from workloads import qwen3
+
+    cfg = qwen3.Qwen3Config()
+    ids = qwen3.tokens(5, 128, cfg.vocab_size)
+    used = []
+    put = qwen3.NormHandoff.put
+
+    def counting_put(self, h, hn):
+        used.append(h.shape[1])
+        put(self, h, hn)
+
+    def run(link):
+        model = qwen3.build(cfg, seed=6, num_layers=3)
+        if link is not None:
+            qwen3.install_regions(model, link_layers=link)
+        caches = model.make_cache(256)
+        a = model(ids, caches)
+        b = model(ids[:, :1], caches)
+        torch.cuda.synchronize()
+        return a, b
+
+    want = run(None)
+    assert all(torch.equal(g, w) for g, w in zip(run(False), want))
+    qwen3.NormHandoff.put = counting_put
+    try:
+        got = run(True)
+    finally:
+        qwen3.NormHandoff.put = put
+    assert all(torch.equal(g, w) for g, w in zip(got, want))
+    assert used == [128, 128, 1, 1], used
+
+
+@pytest.mark.gpu
 @pytest.mark.timeout(900)
 def test_qwen3_model_config4_prefill_and_decode():
     """36 layers + tied quantized embedding/lm_head (V = 151936), prefill of 128
