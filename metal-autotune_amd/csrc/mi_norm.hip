@@ -214,6 +214,15 @@ struct NRJobs {
     int64_t end0, end1, rows;  // cumulative row ends
 };
 
+// The rotation of a pair (a, c) by an angle of cosine cs and sine sn, each
+// output one fma over a rounded product: a cs - c sn and a sn + c cs.
+__device__ __forceinline__ float rope_first(float a, float c, float cs, float sn) {
+    return __builtin_fmaf(a, cs, -(c * sn));
+}
+__device__ __forceinline__ float rope_second(float a, float c, float cs, float sn) {
+    return __builtin_fmaf(a, sn, c * cs);
+}
+
 template <typename T, int R>
 __global__ __launch_bounds__(256) void norm_rope_kernel(NRJobs jobs, int64_t B, int64_t L,
                                                         int64_t D, float eps, int trad,
@@ -238,6 +247,31 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NRJobs jobs, int64_t B, 
     T *orow = out + ((b * H + h) * cap + pos0 + l) * D;
     const int half = dims / 2;
     const int slots = (int)(D / 2);
+    const float position = (float)(l + offset) * scale;
+    if (!trad && D == 2 * R && dims == D) {
+        // Each lane owns elements t and t + R: its two terms of the RMS and
+        // one rotation pair. One load of each, issued with the weights before
+        // the angle math, which then runs under their latency; the same
+        // arithmetic, in the same order, as the general loop below.
+        const float a0 = (float)xr[t], c0 = (float)xr[t + R];
+        const float wa = w ? (float)w[t] : 1.0f, wc = w ? (float)w[t + R] : 1.0f;
+        const float inv_freq = exp2f(-(float)(2 * t) / (float)dims * log2base);
+        float sn, cs;
+        sincosf(position * inv_freq, &sn, &cs);
+        float a = a0, c = c0;
+        if (w) {
+            float ss = __builtin_fmaf(a0, a0, 0.0f);
+            ss = __builtin_fmaf(c0, c0, ss);
+#pragma unroll
+            for (int o = R / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, R);
+            const float inv = 1.0f / __fsqrt_rn(ss / (float)D + eps);
+            a = (float)cvt<T>(wa * (float)cvt<T>(a0 * inv));
+            c = (float)cvt<T>(wc * (float)cvt<T>(c0 * inv));
+        }
+        orow[t] = cvt<T>(rope_first(a, c, cs, sn));
+        orow[t + R] = cvt<T>(rope_second(a, c, cs, sn));
+        return;
+    }
     float inv = 1.0f;
     if (w) {
         float ss = 0.0f;
@@ -249,7 +283,6 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NRJobs jobs, int64_t B, 
         for (int o = R / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, R);
         inv = 1.0f / __fsqrt_rn(ss / (float)D + eps);
     }
-    const float position = (float)(l + offset) * scale;
     for (int p = t; p < slots; p += R) {
         int e0, e1;
         const bool rot = p < half;
@@ -269,8 +302,8 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NRJobs jobs, int64_t B, 
             const float inv_freq = exp2f(-(float)(2 * p) / (float)dims * log2base);
             float sn, cs;
             sincosf(position * inv_freq, &sn, &cs);
-            const float ra = a * cs - c * sn;
-            const float rc = a * sn + c * cs;
+            const float ra = rope_first(a, c, cs, sn);
+            const float rc = rope_second(a, c, cs, sn);
             a = ra;
             c = rc;
         }
