@@ -74,18 +74,17 @@ template <int D> __device__ __forceinline__ void attn_init(AttnState<D> &st) {
     st.l = 0.0f;
 }
 
-// One key tile kt: s = S^T (s[i]: key kt*32 + 8*(i/4) + 4*h2 + i%4 of query
-// row qrow), vts = the tile's V^T in LDS (D rows of ATT_VP). Masking, the
-// lazily rescaled online softmax, O^T += V^T . P^T.
-template <typename T, int D>
-__device__ __forceinline__ void attn_tile(AttnState<D> &st, const f32x16 &s, const T *vts, int kt,
-                                          int64_t q0, int64_t qrow, int64_t off, int64_t Lk,
-                                          int causal, float scale_log2, int h2, int r) {
+// One key tile kt, in two steps. attn_scores: s = S^T (s[i]: key
+// kt*32 + 8*(i/4) + 4*h2 + i%4 of query row qrow) -> masking and the lazily
+// rescaled online softmax; p gets the tile's probabilities. attn_pv:
+// O^T += V^T . P^T, vts = the tile's V^T in LDS (D rows of ATT_VP). attn_tile
+// runs both; the split kernel runs the scores before its V tile is written.
+template <int D>
+__device__ __forceinline__ void attn_scores(AttnState<D> &st, const f32x16 &s, float (&p)[16],
+                                            int kt, int64_t q0, int64_t qrow, int64_t off,
+                                            int64_t Lk, int causal, float scale_log2, int h2) {
 #pragma clang fp contract(off)
     constexpr int DT = D / 32;
-    typedef typename Vec<T>::x8 V8;
-    typedef typename Vec<T>::x4 V4;
-    float p[16];
     float mt = -INFINITY;
     // a tile whose every key every row of the block sees needs no mask
     const bool full = (int64_t)kt * ATT_KT + ATT_KT <= Lk &&
@@ -123,6 +122,15 @@ __device__ __forceinline__ void attn_tile(AttnState<D> &st, const f32x16 &s, con
         psum += p[i];
     }
     st.l += psum;
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void attn_pv(AttnState<D> &st, const float (&p)[16], const T *vts,
+                                        int h2, int r) {
+#pragma clang fp contract(off)
+    constexpr int DT = D / 32;
+    typedef typename Vec<T>::x8 V8;
+    typedef typename Vec<T>::x4 V4;
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
         V8 pb;
@@ -144,38 +152,64 @@ __device__ __forceinline__ void attn_tile(AttnState<D> &st, const f32x16 &s, con
     }
 }
 
-// Fold a later stream's state (mw, lw, ow(t, i)) into st. A stream that saw
-// no visible key of the row (mw = -inf) leaves st as it is.
-template <int D, typename OW>
-__device__ __forceinline__ void attn_merge(AttnState<D> &st, float mw, float lw, OW ow) {
-#pragma clang fp contract(off)
-    if (mw == -INFINITY) return;
-    const float m_new = fmaxf(st.m, mw);
-    const float c0 = st.m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(st.m - m_new);
-    const float cw = __builtin_amdgcn_exp2f(mw - m_new);
-#pragma unroll
-    for (int t = 0; t < D / 32; ++t)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) st.o[t][i] = __builtin_fmaf(st.o[t][i], c0, ow(t, i) * cw);
-    st.l = __builtin_fmaf(st.l, c0, lw * cw);
-    st.m = m_new;
+template <typename T, int D>
+__device__ __forceinline__ void attn_tile(AttnState<D> &st, const f32x16 &s, const T *vts, int kt,
+                                          int64_t q0, int64_t qrow, int64_t off, int64_t Lk,
+                                          int causal, float scale_log2, int h2, int r) {
+    float p[16];
+    attn_scores<D>(st, s, p, kt, q0, qrow, off, Lk, causal, scale_log2, h2);
+    attn_pv<T, D>(st, p, vts, h2, r);
 }
 
-// O = O^T / row sum, stored as the lane's query row.
-template <typename T, int D>
-__device__ __forceinline__ void attn_store(const AttnState<D> &st, T *orow, int h2) {
+// Folding a later stream's state (mw, lw, o_w) into a running (m, l, o):
+// m' = max(m, mw); o' = o c0 + o_w cw and l' = l c0 + lw cw with
+// c0 = 2^(m - m'), cw = 2^(mw - m'). A stream that saw no visible key of the
+// row (mw = -inf) leaves the state as it is.
+struct MergeCoef {
+    float c0, cw, m_new;
+};
+__device__ __forceinline__ MergeCoef merge_coef(float m, float mw) {
 #pragma clang fp contract(off)
-    const float l_tot = st.l + __shfl_xor(st.l, 32, 64);
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    const float m_new = fmaxf(m, mw);
+    return {m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - m_new),
+            __builtin_amdgcn_exp2f(mw - m_new), m_new};
+}
+__device__ __forceinline__ float merge_one(float o, float ow, const MergeCoef &c) {
+#pragma clang fp contract(off)
+    return __builtin_fmaf(o, c.c0, ow * c.cw);
+}
+
+template <int D, typename OW>
+__device__ __forceinline__ void attn_merge(AttnState<D> &st, float mw, float lw, OW ow) {
+    if (mw == -INFINITY) return;
+    const MergeCoef c = merge_coef(st.m, mw);
 #pragma unroll
     for (int t = 0; t < D / 32; ++t)
 #pragma unroll
-        for (int blk = 0; blk < 4; ++blk) {
-            float f[4];
+        for (int i = 0; i < 16; ++i) st.o[t][i] = merge_one(st.o[t][i], ow(t, i), c);
+    st.l = merge_one(st.l, lw, c);
+    st.m = c.m_new;
+}
+
+// Output tile t (features 32 t .. 32 t + 31) of the lane's query row: O^T / row sum.
+template <typename T>
+__device__ __forceinline__ void attn_store_tile(const f32x16 &o, float l, T *orow, int t, int h2) {
+#pragma clang fp contract(off)
+    const float l_tot = l + __shfl_xor(l, 32, 64);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) f[e] = st.o[t][4 * blk + e] * inv;
-            st8(orow + 32 * t + 8 * blk + 4 * h2, pack4<T>(f));
-        }
+    for (int blk = 0; blk < 4; ++blk) {
+        float f[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f[e] = o[4 * blk + e] * inv;
+        st8(orow + 32 * t + 8 * blk + 4 * h2, pack4<T>(f));
+    }
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void attn_store(const AttnState<D> &st, T *orow, int h2) {
+#pragma unroll
+    for (int t = 0; t < D / 32; ++t) attn_store_tile<T>(st.o[t], st.l, orow, t, h2);
 }
 
 // Key tiles visible to a q block (causal: up to its last row).
@@ -195,9 +229,9 @@ template <int D> struct SplitLds {
     static constexpr int DT = D / 32;
     static constexpr int VT_BYTES = D * ATT_VP * 2;            // one wave's V^T tile
     static constexpr int PART_FLOATS = DT * 16 * 64 + 2 * 64;  // one wave's state
-    static constexpr int BYTES = ATT_STREAMS * VT_BYTES > (ATT_STREAMS - 1) * PART_FLOATS * 4
+    static constexpr int BYTES = ATT_STREAMS * VT_BYTES > ATT_STREAMS * PART_FLOATS * 4
                                      ? ATT_STREAMS * VT_BYTES
-                                     : (ATT_STREAMS - 1) * PART_FLOATS * 4;
+                                     : ATT_STREAMS * PART_FLOATS * 4;
 };
 
 template <typename T, int D>
@@ -255,6 +289,16 @@ __global__ __launch_bounds__(64 * ATT_STREAMS) void attn_split_kernel(
     if (wave < ntiles) fetch(wave);
 
     for (int kt = wave; kt < ntiles; kt += ATT_STREAMS) {  // wave-uniform
+        // S^T and the softmax first: the V loads, issued after K's, land
+        // under the MFMAs and the exponentials
+        f32x16 s;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < DS; ++ks)
+            s = AMfma<T>::mma(__builtin_bit_cast(V8, kf[ks]), __builtin_bit_cast(V8, qf[ks]), s);
+        float p[16];
+        attn_scores<D>(st, s, p, kt, q0, qrow, off, Lk, causal, scale_log2, h2);
         // V^T tile: this wave's own LDS, written and read by this wave only
         // (its LDS instructions execute in order)
         const bool vok = (int64_t)kt * ATT_KT + r < Lk;
@@ -265,22 +309,19 @@ __global__ __launch_bounds__(64 * ATT_STREAMS) void attn_split_kernel(
 #pragma unroll
             for (int e = 0; e < 8; ++e) vts[(dc * 8 + e) * ATT_VP + r] = vv[e];
         }
-        f32x16 s;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) s[i] = 0.0f;
-#pragma unroll
-        for (int ks = 0; ks < DS; ++ks)
-            s = AMfma<T>::mma(__builtin_bit_cast(V8, kf[ks]), __builtin_bit_cast(V8, qf[ks]), s);
         if (kt + ATT_STREAMS < ntiles) fetch(kt + ATT_STREAMS);  // under this tile's math
-        attn_tile<T, D>(st, s, vts, kt, q0, qrow, off, Lk, causal, scale_log2, h2, r);
+        attn_pv<T, D>(st, p, vts, h2, r);
     }
 
-    // Merge: waves 1..3 leave (o, l, m) in LDS (over the V^T tiles); wave 0
-    // folds them in, in stream order.
+    // Merge: every wave leaves its stream's (o, l, m) in LDS (over the V^T
+    // tiles); wave w then folds the four streams, in stream order, for O^T
+    // tile t = w (D = 64: tiles 0 and 1) and stores that tile. Each wave
+    // recomputes the same (m, l) chain, so the result is that of one wave
+    // folding every tile.
     float *part = (float *)lds;
     __syncthreads();  // every wave is done with its V^T tile
-    if (wave > 0) {
-        float *pp = part + (size_t)(wave - 1) * L::PART_FLOATS;
+    {
+        float *pp = part + (size_t)wave * L::PART_FLOATS;
 #pragma unroll
         for (int t = 0; t < DT; ++t)
 #pragma unroll
@@ -289,15 +330,26 @@ __global__ __launch_bounds__(64 * ATT_STREAMS) void attn_split_kernel(
         pp[DT * 16 * 64 + 64 + lane] = st.m;
     }
     __syncthreads();
-    if (wave > 0 || !qok) return;
-    for (int w = 1; w < ATT_STREAMS; ++w) {
-        const float *pp = part + (size_t)(w - 1) * L::PART_FLOATS;
-        attn_merge(st, pp[DT * 16 * 64 + 64 + lane], pp[DT * 16 * 64 + lane],
-                   [&](int t, int i) { return pp[(t * 16 + i) * 64 + lane]; });
-    }
+    if (!qok) return;
     T *orow = out_layout ? out + ((b * Lq + qrow) * H + hq) * D
                          : out + ((b * H + hq) * Lq + qrow) * D;
-    attn_store<T, D>(st, orow, h2);
+    for (int t = wave; t < DT; t += ATT_STREAMS) {  // wave-uniform
+        f32x16 o;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[i] = part[(t * 16 + i) * 64 + lane];
+        float m = part[DT * 16 * 64 + 64 + lane], l = part[DT * 16 * 64 + lane];
+        for (int w = 1; w < ATT_STREAMS; ++w) {
+            const float *pp = part + (size_t)w * L::PART_FLOATS;
+            const float mw = pp[DT * 16 * 64 + 64 + lane];
+            if (mw == -INFINITY) continue;
+            const MergeCoef c = merge_coef(m, mw);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[i] = merge_one(o[i], pp[(t * 16 + i) * 64 + lane], c);
+            l = merge_one(l, pp[DT * 16 * 64 + lane], c);
+            m = c.m_new;
+        }
+        attn_store_tile<T>(o, l, orow, t, h2);
+    }
 }
 
 // ---------------------------------------------------------------------------
