@@ -248,12 +248,14 @@ __global__ __launch_bounds__(64 * ATT_STREAMS) void attn_split_kernel(
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h2 = lane >> 5, r = lane & 31;
-    int64_t bid = blockIdx.x;
-    const int64_t nqb = ceil_div(Lq, 32);
+    // block index -> (b, q head, q block) in 32-bit math (grids are far below
+    // 2^31 blocks; 64-bit divisions cost hundreds of scalar instructions)
+    unsigned bid = blockIdx.x;
+    const unsigned nqb = (unsigned)ceil_div(Lq, 32);
     const int64_t qblk = bid % nqb;
     bid /= nqb;
-    const int64_t hq = bid % H, b = bid / H;
-    const int64_t hk = hq / (H / HK);
+    const int64_t hq = bid % (unsigned)H, b = bid / (unsigned)H;
+    const int64_t hk = (unsigned)hq / (unsigned)(H / HK);
     const int64_t q0 = qblk * 32;
     const int64_t off = Lk - Lq;
     const int64_t qrow = q0 + r;
@@ -369,13 +371,13 @@ __global__ __launch_bounds__(256) void attn_shared_kernel(
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int h2 = lane >> 5, r = lane & 31;
-    int64_t bid = blockIdx.x;
-    const int64_t nqb = ceil_div(Lq, 32);
+    unsigned bid = blockIdx.x;  // 32-bit index math, as in attn_split_kernel
+    const unsigned nqb = (unsigned)ceil_div(Lq, 32);
     const int64_t qblk = bid % nqb;
     bid /= nqb;
-    const int quad = (int)(bid % quads);
-    bid /= quads;
-    const int64_t hk = bid % HK, b = bid / HK;
+    const int quad = (int)(bid % (unsigned)quads);
+    bid /= (unsigned)quads;
+    const int64_t hk = bid % (unsigned)HK, b = bid / (unsigned)HK;
     const int64_t rep = H / HK;
     const bool active = quad * 4 + wave < rep;
     const int64_t hq = hk * rep + (active ? quad * 4 + wave : 0);

@@ -23,7 +23,8 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t *__restrict
     const int64_t cpr = K / VPC;     // chunks per row
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= rows * cpr) return;
-    const int64_t r = t / cpr, c = t - r * cpr;
+    // 32-bit index math (the launcher keeps rows * cpr below 2^31)
+    const int64_t r = (unsigned)t / (unsigned)cpr, c = t - r * cpr;
     int64_t n = r;
     if (ids) {
         n = ids64 ? ((const int64_t *)ids)[r] : (int64_t)((const int32_t *)ids)[r];
@@ -31,9 +32,10 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t *__restrict
     }
     const uint4 wv = ld16(w + n * (K / VPW) + c * 4);
     const int64_t k0 = c * VPC;
-    const int64_t G = K / gs;
-    const float sc = (float)s[n * G + k0 / gs];
-    const float bi = (float)b[n * G + k0 / gs];
+    const int gsh = __builtin_ctz((unsigned)gs);  // group sizes are powers of two
+    const int64_t G = K >> gsh;
+    const float sc = (float)s[n * G + (k0 >> gsh)];
+    const float bi = (float)b[n * G + (k0 >> gsh)];
     const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
     float v[VPC];
 #pragma unroll
@@ -65,6 +67,8 @@ int launch_dequant(const uint32_t *w, const void *s, const void *b, void *out, c
     const int vpc = bits == 4 ? 32 : 16;
     const int64_t threads = rows * (K / vpc);
     if (threads == 0) return MI_OK;
+    if (threads >= ((int64_t)1 << 31))  // the kernel indexes threads in 32 bits
+        return fail(MI_ERR_UNSUPPORTED, "dequant of %lld chunks", (long long)threads);
     const dim3 grid((unsigned)ceil_div(threads, 256));
     if (bits == 4)
         dequant_kernel<T, 4><<<grid, 256, 0, st>>>(w, (const T *)s, (const T *)b, (T *)out, ids,

@@ -55,7 +55,9 @@ __global__ __launch_bounds__(256) void shortconv_kernel(const T *__restrict__ bx
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t dchunks = ceil_div(D, 8);
     if (t >= B * (L + 2) * dchunks) return;
-    const int64_t dc = t % dchunks, row = (t / dchunks) % (L + 2), b = t / (dchunks * (L + 2));
+    // 32-bit index math (the launcher keeps the thread count below 2^31)
+    const unsigned ut = (unsigned)t, udc = (unsigned)dchunks, ulr = (unsigned)(L + 2);
+    const int64_t dc = ut % udc, row = (ut / udc) % ulr, b = ut / (udc * ulr);
     if constexpr (VEC && sizeof(T) == 2) {
         const int64_t d0 = dc * 8;
         auto padv = [&](int64_t i, float (&f)[8]) {
@@ -508,6 +510,8 @@ extern "C" int mi_shortconv(const void *bx, const void *c, const void *w, const 
     if (B * L && (!bx || !c || !w || !out)) return fail(MI_ERR_ARG, "null pointer");
     const int64_t threads = B * (L + 2) * ceil_div(D, 8);
     if (threads == 0) return MI_OK;
+    if (threads >= ((int64_t)1 << 31))  // the kernel indexes threads in 32 bits
+        return fail(MI_ERR_UNSUPPORTED, "shortconv of %lld 8-channel chunks", (long long)threads);
     hipStream_t st = as_stream(stream);
     const unsigned grid = (unsigned)ceil_div(threads, 256);
     const bool vec = D % 8 == 0 && aligned(bx, 16) && aligned(c, 16) && aligned(w, 16) &&

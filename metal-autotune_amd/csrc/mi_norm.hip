@@ -242,7 +242,9 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NRJobs jobs, int64_t B, 
     const int64_t cap = a0 ? jobs.j0.cap : (a1 ? jobs.j1.cap : jobs.j2.cap);
     const int64_t pos0 = a0 ? jobs.j0.pos0 : (a1 ? jobs.j1.pos0 : jobs.j2.pos0);
     const int dims = a0 ? jobs.j0.dims : (a1 ? jobs.j1.dims : jobs.j2.dims);
-    const int64_t h = row % H, l = (row / H) % L, b = row / (H * L);
+    // (32-bit: rows < 2^31; a 64-bit division per lane costs tens of VALU)
+    const unsigned ur = (unsigned)row, uh = (unsigned)H, ul = (unsigned)L;
+    const int64_t h = ur % uh, l = (ur / uh) % ul, b = ur / (uh * ul);
     const T *xr = x + (b * L + l) * xs + h * D;
     T *orow = out + ((b * H + h) * cap + pos0 + l) * D;
     const int half = dims / 2;
@@ -317,6 +319,8 @@ int launch_norm_rope(const NRJobs &jobs, int64_t B, int64_t L, int64_t D, float 
                      float log2base, float scale, int64_t offset, hipStream_t st) {
     const int64_t rows = jobs.rows;
     if (rows == 0) return MI_OK;
+    if (rows >= ((int64_t)1 << 31))  // the kernel splits a row index in 32 bits
+        return fail(MI_ERR_UNSUPPORTED, "norm_rope of %lld rows", (long long)rows);
     const int64_t slots = D / 2;
 #define MI_NR_LAUNCH(RR)                                                                       \
     norm_rope_kernel<T, RR><<<(unsigned)ceil_div(rows, 256 / RR), 256, 0, st>>>(                \

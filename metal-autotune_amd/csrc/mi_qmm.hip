@@ -57,6 +57,8 @@ struct QParams {
     int wk;                    // K-split waves (qmm_mfma_kernel)
     int sbp;                   // qmm_mfma_kernel: groups per row of a wave's scale/bias table
     int n4;                    // qmm_mfma_mixed_kernel: feature tiles taken as 128-token tiles
+    int sbninst;               // qmm_mfma_kernel: DMA instructions per scale/bias table array
+    unsigned sbmagic;          // ceil(2^20 / (sbp / 2)): v / (sbp / 2) as (v * sbmagic) >> 20
     int ks;                    // K parts (kpart_count): each is split over the wk waves
     int kslice;                // k values of the longest wave chunk (ks * wk chunks of K)
     float *part;               // non-null: write K part blockIdx.z's sums, fp32 [ks, M, Nout]
@@ -225,7 +227,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QParams p) {
     const Bound bd = bind<EPI>(p, nb);
     const int64_t n = nb + (threadIdx.x >> 6) * 4 + (lane >> 4);
     const int64_t m0 = (int64_t)blockIdx.y * MR;
-    const int64_t K = p.K, cpr = K / VPC, G = K / p.gs;
+    const int64_t K = p.K, cpr = K / VPC, G = K >> p.gs_log2;
     const int mr = (int)((p.M - m0) < MR ? (p.M - m0) : MR);
     const T *x = (const T *)p.x + m0 * K;
 
@@ -349,7 +351,7 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
     constexpr int P = epi_parts(EPI);
     typedef Magic<T> Mg;
     extern __shared__ uint4 xs_pairs[];  // [MR][K/8] pair blocks, then [MR][K/32] sums
-    const int64_t K = p.K, words = K / 8, cpr = K / 32, G = K / p.gs;
+    const int64_t K = p.K, words = K / 8, cpr = K / 32, G = K >> p.gs_log2;
     float *xsum = (float *)(xs_pairs + MR * words);
     const int lane = threadIdx.x & 63, j = lane & 15;
     int64_t nb = (int64_t)blockIdx.x * 16;
@@ -416,14 +418,16 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
             if (idx < MR * words) xs_pairs[idx] = pairs(d[t]);
         }
     } else {
-        for (int64_t idx = threadIdx.x; idx < MR * words; idx += 256) {
-            const int64_t m = idx / words, w = idx - m * words;
-            xs_pairs[idx] = pairs(ld16(x + (m < mr ? m : mr - 1) * K + 8 * w));
+        const int nw = (int)words;  // 32-bit index math: MR * K < 2^31
+        for (int idx = threadIdx.x; idx < MR * nw; idx += 256) {
+            const int m = MR == 1 ? 0 : idx / nw, w = idx - m * nw;
+            xs_pairs[idx] = pairs(ld16(x + (int64_t)(m < mr ? m : mr - 1) * K + 8 * w));
         }
     }
     __syncthreads();
-    for (int64_t idx = threadIdx.x; idx < MR * cpr; idx += 256) {
-        const int64_t m = idx / cpr, c = idx - m * cpr;
+    const int ncpr = (int)cpr;
+    for (int idx = threadIdx.x; idx < MR * ncpr; idx += 256) {
+        const int m = MR == 1 ? 0 : idx / ncpr, c = idx - m * ncpr;
         float s = 0.0f;
 #pragma unroll
         for (int wi = 0; wi < 4; ++wi) {
@@ -669,11 +673,14 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
     // Wave kw owns chunk kw of each K part.
     const int kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = lane >> 5, r = lane & 31;
-    const int64_t K = p.K, G = K / p.gs;
+    const int64_t K = p.K, G = K >> p.gs_log2;
     int64_t n_wave = n_blk;
     const Bound bd = bind<EPI>(p, n_wave);
     const int wk = p.wk;
+    // chunks = ks * wk is a power of two (ks, wk in {1, 2, 4}): chunk
+    // boundaries are a shift, not a division
     const int chunks = (KM == KM_ONE ? 1 : p.ks) * wk, nstages = (int)(K / XK);
+    const int cshift = __builtin_ctz((unsigned)chunks);
     const int nparts = KM == KM_LOOP ? p.ks : 1;  // K parts this workgroup runs
     char *xbuf = lds + kw * Sh::STAGE;
     const int wslot = Sh::XST;  // this wave's weights within its slot
@@ -700,7 +707,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
         woff[a] = (uint32_t)(tile_row(a, r) * (K * BITS / 8) + 16 * h);
     }
     const int pitch = p.sbp;
-    const SbtLayout tl = sbt_layout(p.kslice, p.gs);
+    const SbtLayout tl = {pitch, p.sbninst, p.sbninst * 256};  // sbt_layout(p.kslice, p.gs)
     extern __shared__ __attribute__((aligned(16))) char lds_dyn[];
     const char *sbt = lds_dyn + kw * (A * 2 * tl.array_bytes);
     float *psum = (float *)(lds_dyn + wk * (A * 2 * tl.array_bytes));  // sums over K parts
@@ -725,9 +732,9 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
     f32x16 acc[A][C];
     for (int kp = 0; kp < nparts; ++kp) {  // workgroup-uniform
         const int cix = (KM == KM_PART ? kz : kp) * wk + kw;
-        const int sbeg = (int)((int64_t)cix * nstages / chunks);
+        const int sbeg = (cix * nstages) >> cshift;
         const int kbeg = sbeg * XK;
-        const int nst = (int)((int64_t)(cix + 1) * nstages / chunks) - sbeg;
+        const int nst = (((cix + 1) * nstages) >> cshift) - sbeg;
         // Scale/bias table (layout in sbt_layout): dword v of an array holds
         // groups gbase + 2j, +1 of tile row v / (pitch / 2), j = v % (pitch / 2).
         // Issued before the ring prologue, so the first stage's wait covers it.
@@ -735,7 +742,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
         for (int i = 0; i < tl.ninst; ++i) {
             int v = 64 * i + lane;
             v = v < 16 * pitch ? v : 16 * pitch - 1;
-            const int rr = v / (pitch >> 1), j = v - rr * (pitch >> 1);
+            const int rr = (int)(((unsigned)v * p.sbmagic) >> 20), j = v - rr * (pitch >> 1);
 #pragma unroll
             for (int a = 0; a < A; ++a) {
                 const uint32_t off = (uint32_t)((tile_row(a, rr) * G + gbase + 2 * j) * 2);
@@ -1078,14 +1085,14 @@ __attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<A, C>()))) void qmm_mfma_ke
 // one XCD and all but the first read the weight tile from its L2 (adjacent
 // blocks fetched every weight byte g times from HBM). Groups of 8 tiles take
 // 8 g blocks; a last partial group of r tiles spaces its blocks r apart.
-__device__ __forceinline__ void mixed_tile_of(int64_t i, int64_t n, int g, int64_t &j,
-                                              int64_t &part) {
-    const int64_t full = 8 * g * (n / 8);
+__device__ __forceinline__ void mixed_tile_of(int i, int n, int g, int64_t &j, int64_t &part) {
+    // 32-bit index math (grids are far below 2^31 blocks); g is 1, 2 or 4
+    const int full = 8 * g * (n / 8);
     if (i < full) {
         j = 8 * (i / (8 * g)) + i % 8;
         part = (i / 8) % g;
     } else {
-        const int64_t rem = n % 8, t = i - full;
+        const unsigned rem = (unsigned)(n % 8), t = (unsigned)(i - full);
         j = 8 * (n / 8) + t % rem;
         part = t / rem;
     }
@@ -1124,11 +1131,11 @@ __attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<A, CB>()))) void qmm_mfma_m
             return;
         }
     } else if (b < nb * GB) {
-        mixed_tile_of(b, nb, GB, j, part);
+        mixed_tile_of((int)b, (int)nb, GB, j, part);
         qmm_mfma_tile<T, BITS, A, CB, 4, EPI>(p, lds, j * (32 * TN), part * 32 * CB);
         return;
     }
-    mixed_tile_of(b - nb * GB, nt - nb, GS, j, part);
+    mixed_tile_of((int)(b - nb * GB), (int)(nt - nb), GS, j, part);
     qmm_mfma_tile<T, BITS, A, CS, 4, EPI>(p, lds, (nb + j) * (32 * TN), part * 32 * CS);
 }
 
@@ -1164,8 +1171,11 @@ inline int64_t mfma_sum_bytes(const QParams &p, int A, int C) {
 
 // Dynamic LDS of one workgroup: the waves' scale/bias tables and the sums
 // over the K parts.
+// (a table too long for the index multiplier of set_table counts as not
+// fitting, so the dispatcher takes another kernel)
 inline int64_t mfma_dyn_bytes(const QParams &p, int A, int C, int wk) {
     const SbtLayout tl = sbt_layout(kslice_of(p.K, p.ks, wk), p.gs);
+    if (8ll * tl.pitch * tl.pitch >= (1ll << 20)) return 1ll << 40;
     return (int64_t)wk * A * 2 * tl.array_bytes + mfma_sum_bytes(p, A, C);
 }
 
@@ -1175,14 +1185,27 @@ int64_t mfma_lds_bytes(const QParams &p, int wk) {
     return MfmaShape<T, BITS, A, C, 4>::LDS + mfma_dyn_bytes(p, A, C, wk);
 }
 
+// The scale/bias table fields of p for wk waves: the longest chunk, the
+// table layout, and the multiplier that divides a table dword index by
+// pitch / 2 (exact for indices below 16 pitch while 8 pitch^2 < 2^20, i.e.
+// K slices up to 360 groups; the host refuses longer ones).
+inline bool set_table(QParams &p, int wk) {
+    p.kslice = kslice_of(p.K, p.ks, wk);
+    const SbtLayout tl = sbt_layout(p.kslice, p.gs);
+    p.sbp = tl.pitch;
+    p.sbninst = tl.ninst;
+    const unsigned half = (unsigned)(tl.pitch / 2);
+    p.sbmagic = ((1u << 20) + half - 1) / half;
+    return 8ll * tl.pitch * tl.pitch < (1ll << 20);
+}
+
 // p.ks K parts in grid z when p.part is set, else each workgroup runs them.
 template <typename T, int BITS, int A, int C, int EPI, int KM = KM_ONE>
 int launch_mfma_cfg(QParams p, int wk, hipStream_t st) {
     constexpr int P = epi_parts(EPI);
     constexpr int TN = (P == 1) ? A : 1;
     p.wk = wk;
-    p.kslice = kslice_of(p.K, p.ks, wk);
-    p.sbp = sbt_layout(p.kslice, p.gs).pitch;
+    set_table(p, wk);
     const size_t dyn = (size_t)mfma_dyn_bytes(p, A, C, wk);
     if (mfma_lds_bytes<T, BITS, A, C>(p, wk) > LDS_PER_CU)
         return fail(MI_ERR_UNSUPPORTED, "quantized matmul tile exceeds the LDS (K = %lld)",
@@ -1213,8 +1236,7 @@ int device_cus() {
 template <typename T, int BITS, int A, int EPI, int CB>
 int launch_mfma_mixed(QParams p, int nb, int64_t nt, hipStream_t st) {
     p.wk = 4;
-    p.kslice = kslice_of(p.K, p.ks, 4);
-    p.sbp = sbt_layout(p.kslice, p.gs).pitch;
+    set_table(p, 4);
     p.n4 = nb;
     const size_t dyn = (size_t)mfma_dyn_bytes(p, A, CB, 4);
     const unsigned blocks = (unsigned)(nb * (4 / CB) + (nt - nb) * (8 / CB));
@@ -1245,8 +1267,7 @@ int launch_mfma(const QParams &p, hipStream_t st) {
     if (p.ks > 1) {
         if (mfma_lds_bytes<T, BITS, P, 1>(p, wk) <= LDS_PER_CU)
             return launch_mfma_cfg<T, BITS, P, 1, EPI, KM_LOOP>(p, wk, st);
-        return fail(MI_ERR_UNSUPPORTED, "quantized matmul tile exceeds the LDS (K = %lld)",
-                    (long long)p.K);
+        return launch_qmv<T, BITS, EPI>(p, st);
     }
     const int64_t nt = ceil_div(p.Nout, 32);
     const bool large = p.M >= 512 || nt * ceil_div(p.M, 64) > 2048;
@@ -1446,6 +1467,10 @@ int64_t qmm_parts_bytes(int64_t M, int64_t N, int64_t K, int gs, int bits, int d
         return 0;
     const int ks = kpart_count(M, K);
     if (ks < 2 || N % 4 || !mfma_shape_ok(M, K, N, gs, bits)) return 0;
+    const int64_t stages = K / XK;
+    const int wk = (stages % 4 == 0) ? 4 : (stages % 2 == 0 ? 2 : 1);
+    const int pitch = sbt_layout(kslice_of(K, ks, wk), gs).pitch;
+    if (8ll * pitch * pitch >= (1ll << 20)) return 0;  // (the one-launch path takes it)
     return (int64_t)ks * M * N * (int64_t)sizeof(float);
 }
 
