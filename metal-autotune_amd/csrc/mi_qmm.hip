@@ -1391,7 +1391,8 @@ __global__ __launch_bounds__(256) void qmm_parts_sum_kernel(QParams p) {
     const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t size = p.M * p.Nout;
     if (4 * q >= size) return;
-    const int64_t o = 4 * q, m = o / p.Nout, n = o - m * p.Nout;
+    // 32-bit row split: M * Nout < 2^31 (qmm_parts_bytes)
+    const int64_t o = 4 * q, m = (unsigned)o / (unsigned)p.Nout, n = o - m * p.Nout;
     float4 v = *(const float4 *)(p.part + o);
     float s[1][4] = {{v.x, v.y, v.z, v.w}};
     for (int z = 1; z < p.ks; ++z) {
@@ -1466,7 +1467,8 @@ int64_t qmm_parts_bytes(int64_t M, int64_t N, int64_t K, int gs, int bits, int d
     if ((bits != 4 && bits != 8) || (gs != 32 && gs != 64 && gs != 128) || M < 0 || N <= 0)
         return 0;
     const int ks = kpart_count(M, K);
-    if (ks < 2 || N % 4 || !mfma_shape_ok(M, K, N, gs, bits)) return 0;
+    if (ks < 2 || N % 4 || !mfma_shape_ok(M, K, N, gs, bits) || M * N >= ((int64_t)1 << 31))
+        return 0;
     const int64_t stages = K / XK;
     const int wk = (stages % 4 == 0) ? 4 : (stages % 2 == 0 ? 2 : 1);
     const int pitch = sbt_layout(kslice_of(K, ks, wk), gs).pitch;
