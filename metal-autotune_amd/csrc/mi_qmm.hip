@@ -959,6 +959,93 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
         // the reduction or released with the workgroup
         wait_vmcnt<0>();
 
+        if constexpr (KM != KM_LOOP) {
+            static_assert(Sh::KG == 4, "one-part tiles split K over four waves");
+            {  // (the host launches these with wk = 4)
+                // The four partial tiles reduced by all four waves: in round q
+                // every wave leaves quarter q of its tile (acc[.][.][4q .. 4q+3],
+                // features 8q + 4h .. +3 of each 32x32 tile) in LDS, and wave q
+                // adds the four, ((p0 + p1) + p2) + p3 -- the sums of a one-wave
+                // reduction -- into the registers of its quarter 0 (already
+                // handed over in round 0), then stores them as quarter q. Each
+                // wave reads a quarter of the partials and runs a quarter of the
+                // epilogue.
+                // Two buffers alternate (one for three-part tiles, whose slots
+                // hold one): a round's writes reach a buffer only after the
+                // barrier that follows its previous reader's read.
+                constexpr int QV = A * C * 4;  // floats per lane and quarter
+                constexpr int NBUF = A <= 2 ? 2 : 1;
+                static_assert(NBUF * 4 * QV * 64 * 4 <= Sh::LDS, "reduction buffers exceed the slots");
+                float *red = (float *)lds;
+                __syncthreads();  // every wave is done with its slot
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float *buf = red + (q % NBUF) * (4 * QV * 64);
+                    if (NBUF == 1 && q > 0) __syncthreads();  // wave q - 1 has read it
+#pragma unroll
+                    for (int a = 0; a < A; ++a)
+#pragma unroll
+                        for (int c = 0; c < C; ++c)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                buf[(kw * QV + (a * C + c) * 4 + e) * 64 + lane] = acc[a][c][4 * q + e];
+                    __syncthreads();
+                    if (kw == q) {
+#pragma unroll
+                        for (int a = 0; a < A; ++a)
+#pragma unroll
+                            for (int c = 0; c < C; ++c)
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) {
+                                    const float *bp = buf + ((a * C + c) * 4 + e) * 64 + lane;
+                                    float v = bp[0];
+                                    v += bp[QV * 64];
+                                    v += bp[2 * QV * 64];
+                                    v += bp[3 * QV * 64];
+                                    acc[a][c][e] = v;
+                                }
+                    }
+                }
+                const int blk = kw;  // this wave's quarter
+                if constexpr (KM == KM_PART) {
+                    float *dst = p.part + (int64_t)kz * p.M * bd.Nout;
+#pragma unroll
+                    for (int c = 0; c < C; ++c) {
+                        const int64_t m = m_blk + 32 * c + r;
+#pragma unroll
+                        for (int a = 0; a < A; ++a) {
+                            const int64_t n = n_wave + 32 * a + 8 * blk + 4 * h;
+                            if (m < p.M && n < bd.Nout)
+                                *(float4 *)(dst + m * bd.Nout + n) =
+                                    make_float4(acc[a][c][0], acc[a][c][1], acc[a][c][2],
+                                                acc[a][c][3]);
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int c = 0; c < C; ++c) {
+                        const int64_t m = m_blk + 32 * c + r;
+                        if constexpr (P == 1) {
+#pragma unroll
+                            for (int a = 0; a < A; ++a) {
+                                float v[1][4] = {{acc[a][c][0], acc[a][c][1], acc[a][c][2],
+                                                  acc[a][c][3]}};
+                                epi4<T, EPI, 1>(p, bd, m, n_wave + 32 * a + 8 * blk + 4 * h, v);
+                            }
+                        } else {
+                            float v[P][4];
+#pragma unroll
+                            for (int q = 0; q < P; ++q)
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) v[q][e] = acc[q][c][e];
+                            epi4<T, EPI, P>(p, bd, m, n_wave + 8 * blk + 4 * h, v);
+                        }
+                    }
+                }
+                return;
+            }
+        }
+
         if constexpr (Sh::KG > 1) {
             // Fixed-order reduction of the K-split partial tiles: K-group 0 adds
             // groups 1, 2, ... in turn. The ring's LDS is reused, RSLOTS partials
@@ -1260,8 +1347,9 @@ int launch_mfma_mixed(QParams p, int nb, int64_t nt, hipStream_t st) {
 template <typename T, int BITS, int EPI>
 int launch_mfma(const QParams &p, hipStream_t st) {
     constexpr int P = epi_parts(EPI);
-    const int64_t stages = p.K / XK;
-    const int wk = (stages % 4 == 0) ? 4 : (stages % 2 == 0 ? 2 : 1);
+    // four K-split waves (chunks of whole stages, as even as the stage count
+    // allows; one-part tiles reduce them across the four waves)
+    const int wk = 4;
     // Several K parts without a workspace: each workgroup runs them in turn,
     // on 32-token tiles (the _ws entries run them as workgroups of their own)
     if (p.ks > 1) {
@@ -1296,7 +1384,7 @@ int launch_mfma(const QParams &p, hipStream_t st) {
     // workgroup takes as long as two smaller ones sharing a CU.
     if constexpr (BITS == 4 && P <= 2) {
         const int64_t cus = device_cus();
-        if (p.M > 64 && p.M <= 128 && wk == 4) {
+        if (p.M > 64 && p.M <= 128) {
             if constexpr (P == 2) {
                 const int64_t nb4 = 2 * nt - 2 * cus;  // 128-token tiles
                 if (nb4 > 0 && nb4 <= cus && 2 * mfma_lds_bytes<T, BITS, P, 4>(p, wk) <= LDS_PER_CU)
@@ -1370,8 +1458,7 @@ int launch_typed(const QParams &p, int bits, hipStream_t st) {
 // sums, and the epilogue runs in the kernel that adds them.
 template <typename T, int BITS>
 int launch_parts(const QParams &p, hipStream_t st) {
-    const int64_t stages = p.K / XK;
-    const int wk = (stages % 4 == 0) ? 4 : (stages % 2 == 0 ? 2 : 1);
+    const int wk = 4;
     const int C = p.M > 64 ? 4 : (p.M > 32 ? 2 : 1);
     const bool a2 = ceil_div(p.Nout, 64) * ceil_div(p.M, 32 * C) * p.ks >= 128;
     if constexpr (BITS == 4) {  // (the 8-bit 64x128 tile spills)
@@ -1469,9 +1556,7 @@ int64_t qmm_parts_bytes(int64_t M, int64_t N, int64_t K, int gs, int bits, int d
     const int ks = kpart_count(M, K);
     if (ks < 2 || N % 4 || !mfma_shape_ok(M, K, N, gs, bits) || M * N >= ((int64_t)1 << 31))
         return 0;
-    const int64_t stages = K / XK;
-    const int wk = (stages % 4 == 0) ? 4 : (stages % 2 == 0 ? 2 : 1);
-    const int pitch = sbt_layout(kslice_of(K, ks, wk), gs).pitch;
+    const int pitch = sbt_layout(kslice_of(K, ks, 4), gs).pitch;
     if (8ll * pitch * pitch >= (1ll << 20)) return 0;  // (the one-launch path takes it)
     return (int64_t)ks * M * N * (int64_t)sizeof(float);
 }
