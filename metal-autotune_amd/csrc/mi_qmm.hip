@@ -962,48 +962,65 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
         if constexpr (KM != KM_LOOP) {
             static_assert(Sh::KG == 4, "one-part tiles split K over four waves");
             {  // (the host launches these with wk = 4)
-                // The four partial tiles reduced by all four waves: in round q
-                // every wave leaves quarter q of its tile (acc[.][.][4q .. 4q+3],
-                // features 8q + 4h .. +3 of each 32x32 tile) in LDS, and wave q
-                // adds the four, ((p0 + p1) + p2) + p3 -- the sums of a one-wave
-                // reduction -- into the registers of its quarter 0 (already
-                // handed over in round 0), then stores them as quarter q. Each
-                // wave reads a quarter of the partials and runs a quarter of the
-                // epilogue.
-                // Two buffers alternate (one for three-part tiles, whose slots
-                // hold one): a round's writes reach a buffer only after the
-                // barrier that follows its previous reader's read.
-                constexpr int QV = A * C * 4;  // floats per lane and quarter
-                constexpr int NBUF = A <= 2 ? 2 : 1;
-                static_assert(NBUF * 4 * QV * 64 * 4 <= Sh::LDS, "reduction buffers exceed the slots");
-                float *red = (float *)lds;
+                // The four partial tiles reduced by all four waves. Quarter q of
+                // a tile is acc[.][.][4q .. 4q+3] (features 8q + 4h .. +3 of each
+                // 32x32 tile); every wave leaves its quarters in LDS as 16-byte
+                // words, QPR quarters per round (as many as the slots hold), and
+                // wave q adds the four copies of quarter q, ((p0 + p1) + p2) + p3
+                // -- the sums of a one-wave reduction -- into the registers of
+                // its own quarter 0 (handed over in the first round), then runs
+                // the epilogue for quarter q. Each wave thus reads a quarter of
+                // the partials and runs a quarter of the epilogue.
+                constexpr int AC = A * C;
+                constexpr int QPR = 4 * 4 * AC * 1024 <= Sh::LDS   ? 4
+                                    : 4 * 2 * AC * 1024 <= Sh::LDS ? 2
+                                                                   : 1;
+                static_assert(4 * QPR * AC * 1024 <= Sh::LDS, "reduction exceeds the slots");
+                float4 *red = (float4 *)lds;  // [wave][quarter in round][a * C + c][lane]
                 __syncthreads();  // every wave is done with its slot
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    float *buf = red + (q % NBUF) * (4 * QV * 64);
-                    if (NBUF == 1 && q > 0) __syncthreads();  // wave q - 1 has read it
+                for (int q0 = 0; q0 < 4; q0 += QPR) {
+                    if (q0 > 0) __syncthreads();  // the previous round's readers are done
 #pragma unroll
-                    for (int a = 0; a < A; ++a)
-#pragma unroll
-                        for (int c = 0; c < C; ++c)
-#pragma unroll
-                            for (int e = 0; e < 4; ++e)
-                                buf[(kw * QV + (a * C + c) * 4 + e) * 64 + lane] = acc[a][c][4 * q + e];
-                    __syncthreads();
-                    if (kw == q) {
+                    for (int k = 0; k < QPR; ++k)
 #pragma unroll
                         for (int a = 0; a < A; ++a)
 #pragma unroll
-                            for (int c = 0; c < C; ++c)
+                            for (int c = 0; c < C; ++c) {
+                                const int q = q0 + k;
+                                red[((kw * QPR + k) * AC + a * C + c) * 64 + lane] =
+                                    make_float4(acc[a][c][4 * q], acc[a][c][4 * q + 1],
+                                                acc[a][c][4 * q + 2], acc[a][c][4 * q + 3]);
+                            }
+                    __syncthreads();
 #pragma unroll
-                                for (int e = 0; e < 4; ++e) {
-                                    const float *bp = buf + ((a * C + c) * 4 + e) * 64 + lane;
-                                    float v = bp[0];
-                                    v += bp[QV * 64];
-                                    v += bp[2 * QV * 64];
-                                    v += bp[3 * QV * 64];
-                                    acc[a][c][e] = v;
-                                }
+                    for (int k = 0; k < QPR; ++k) {
+                        if (kw != q0 + k) continue;  // wave-uniform
+#pragma unroll
+                        for (int a = 0; a < A; ++a)
+#pragma unroll
+                            for (int c = 0; c < C; ++c) {
+                                const float4 *bp = red + (k * AC + a * C + c) * 64 + lane;
+                                const int ws = QPR * AC * 64;  // one wave's words
+                                float4 v = bp[0];
+                                const float4 v1 = bp[ws], v2 = bp[2 * ws], v3 = bp[3 * ws];
+                                v.x += v1.x;
+                                v.y += v1.y;
+                                v.z += v1.z;
+                                v.w += v1.w;
+                                v.x += v2.x;
+                                v.y += v2.y;
+                                v.z += v2.z;
+                                v.w += v2.w;
+                                v.x += v3.x;
+                                v.y += v3.y;
+                                v.z += v3.z;
+                                v.w += v3.w;
+                                acc[a][c][0] = v.x;
+                                acc[a][c][1] = v.y;
+                                acc[a][c][2] = v.z;
+                                acc[a][c][3] = v.w;
+                            }
                     }
                 }
                 const int blk = kw;  // this wave's quarter
