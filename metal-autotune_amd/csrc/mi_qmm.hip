@@ -1243,6 +1243,43 @@ __attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<A, CB>()))) void qmm_mfma_m
     qmm_mfma_tile<T, BITS, A, CS, 4, EPI>(p, lds, (nb + j) * (32 * TN), part * 32 * CS);
 }
 
+// Three tile sizes for 64 < M <= 128 when the feature tiles outnumber the CUs
+// by at most a quarter (cus < nt <= 5 cus / 4): a grid of exactly two
+// workgroups per CU, block i and block cus + i sharing a CU. The first nb =
+// 4 (nt - cus) feature tiles are 128-token tiles (blocks 0 .. nb - 1), each
+// sharing its CU with a 32-token quarter of one of the last nb / 4 tiles
+// (blocks cus .. cus + nb - 1, a tile's four quarters 8 blocks apart, on one
+// XCD); the other tiles are 64-token pairs whose halves share a CU (blocks i
+// and cus + i). Every CU then holds 160 or 128 tokens' worth of one feature
+// tile's work, where the two-size grid left some CUs with 192 (a 128-token
+// tile beside a 64-token one) and others with 128. The M = 128 dual (N =
+// 9728, 256 CUs: 192 + 64 pairs + 48 quads) went 26.3-28.3 -> 24.3-25.5 us
+// (A/B on one box), with the same bits.
+template <typename T, int BITS, int A, int EPI>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<A, 4>()))) void qmm_mfma_mixed3_kernel(
+    QParams p) {
+    constexpr int TN = (epi_parts(EPI) == 1) ? A : 1;
+    __shared__ __attribute__((aligned(16))) char lds[MfmaShape<T, BITS, A, 4, 4>::LDS];
+    const int b = (int)blockIdx.x, nb = p.n4, cus = (int)(gridDim.x >> 1);
+    if (b < nb) {  // 128-token tiles
+        qmm_mfma_tile<T, BITS, A, 4, 4, EPI>(p, lds, (int64_t)b * (32 * TN), 0);
+        return;
+    }
+    if (b < cus) {  // first halves of the pairs
+        qmm_mfma_tile<T, BITS, A, 2, 4, EPI>(p, lds, (int64_t)b * (32 * TN), 0);
+        return;
+    }
+    if (b < cus + nb) {  // quarters of the last nb / 4 tiles
+        int64_t j, part;
+        mixed_tile_of(b - cus, nb >> 2, 4, j, part);
+        qmm_mfma_tile<T, BITS, A, 1, 4, EPI>(p, lds, (cus + j) * (32 * TN), part * 32);
+        return;
+    }
+    // second halves of the pairs
+    qmm_mfma_tile<T, BITS, A, 2, 4, EPI>(p, lds, (int64_t)(b - cus) * (32 * TN), 64);
+}
+
 // ---------------------------------------------------------------------------
 // dispatch
 
@@ -1348,6 +1385,18 @@ int launch_mfma_mixed(QParams p, int nb, int64_t nt, hipStream_t st) {
     return launch_status("quantized matmul (mfma, mixed tiles)");
 }
 
+// qmm_mfma_mixed3_kernel: 2 cus blocks, the first nb = 4 (nt - cus) feature
+// tiles as 128-token tiles.
+template <typename T, int BITS, int A, int EPI>
+int launch_mfma_mixed3(QParams p, int nb, int cus, hipStream_t st) {
+    p.wk = 4;
+    set_table(p, 4);
+    p.n4 = nb;
+    const size_t dyn = (size_t)mfma_dyn_bytes(p, A, 4, 4);
+    qmm_mfma_mixed3_kernel<T, BITS, A, EPI><<<(unsigned)(2 * cus), 256, dyn, st>>>(p);
+    return launch_status("quantized matmul (mfma, three tile sizes)");
+}
+
 // Tile choice (measured on MI355X over the Qwen3 prefill shapes, M = 128): one
 // 32-feature tile per part (A = P) and 64-token tiles (C = 2) -- the smallest
 // tiles that still reuse each x fragment across two MFMA columns -- give the
@@ -1394,7 +1443,8 @@ int launch_mfma(const QParams &p, hipStream_t st) {
     // more on some CUs than on others: mixed tiles make it exactly two per CU,
     // at most one of the larger workgroups on each, when two of them fit a
     // CU's LDS (4-bit; the 8-bit 128-token dual tile spills).
-    // - more than two per CU (dual outputs): 128/64-token tiles;
+    // - more than two per CU (dual outputs): 128/64/32-token tiles while the
+    //   feature tiles outnumber the CUs by at most a quarter, else 128/64;
     // - between one and one and a half per CU: 64/32-token tiles.
     // Aiming at one per CU does not pay: q/k/v at M = 128 with 128/64-token
     // tiles, 384 -> 256 workgroups, went 15.2 -> 15.4 us; a lone larger
@@ -1403,6 +1453,12 @@ int launch_mfma(const QParams &p, hipStream_t st) {
         const int64_t cus = device_cus();
         if (p.M > 64 && p.M <= 128) {
             if constexpr (P == 2) {
+                // up to a quarter more feature tiles than CUs: three sizes
+                // (every workgroup allocates the 128-token tile's LDS)
+                const int64_t nq = nt - cus;  // tiles cut into 32-token quarters
+                if (nq > 0 && 4 * nq <= cus && cus % 8 == 0 &&
+                    2 * mfma_lds_bytes<T, BITS, P, 4>(p, wk) <= LDS_PER_CU)
+                    return launch_mfma_mixed3<T, BITS, P, EPI>(p, (int)(4 * nq), (int)cus, st);
                 const int64_t nb4 = 2 * nt - 2 * cus;  // 128-token tiles
                 if (nb4 > 0 && nb4 <= cus && 2 * mfma_lds_bytes<T, BITS, P, 4>(p, wk) <= LDS_PER_CU)
                     return launch_mfma_mixed<T, BITS, P, EPI, 4>(p, (int)nb4, nt, st);

@@ -357,13 +357,14 @@ def test_qmm_dual_and_swiglu(M):
 @pytest.mark.parametrize("M,N", [(128, 9728), (100, 9728), (128, 8704), (128, 5120)])
 def test_qmm_dual_mixed_tiles_equal_plain_tiles(M, N):
     """64 < M <= 128 whose 64-token grid puts one workgroup more on some CUs
-    runs a mixed grid. On MI355X's 256 CUs, N = 9728 (608 workgroups) and
-    N = 8704 (544) take 128-token tiles for the first feature tiles and
-    64-token pairs after; N = 5120 (320) takes 64-token pairs and 32-token
-    quads. Tiles never change results, so it equals, bit for bit, rows
-    [0, 64) and [64, M) from two launches of at most 64 rows (the plain
-    64-token grid); and features at both ends (both tile kinds) are within
-    tolerance of the oracle."""
+    runs a mixed grid. On MI355X's 256 CUs, N = 9728 (304 feature tiles) and
+    N = 8704 (272) take 128-token tiles for the first feature tiles, 64-token
+    pairs after them and 32-token quarters for the last ones; N = 5120 (160)
+    takes 64-token pairs and 32-token quads. Tiles never change results, so
+    it equals, bit for bit, rows [0, 64) and [64, M) from two launches of at
+    most 64 rows (the plain 64-token grid); every output element is written
+    (a NaN-filled output comes back equal); and features at both ends (the
+    first and last tile kinds) are within tolerance of the oracle."""
     r = rng(760 + M + N)
     K = 2560
     x = oracle.round_to(r.normal(0, 1, (1, M, K)), "bfloat16")
@@ -378,6 +379,10 @@ def test_qmm_dual_mixed_tiles_equal_plain_tiles(M, N):
     sw = ops.qmm_dual(xd, *w, swiglu=True)
     sw_parts = [ops.qmm_dual(part, *w, swiglu=True) for part in (lo_x, hi_x)]
     assert torch.equal(sw, torch.cat(sw_parts, dim=1))
+    # every tile of the grid is written: a NaN-filled output comes back whole
+    poisoned = torch.full_like(sw, float("nan"))
+    hip.b_qmm_dual([xd, *w], [poisoned], {**ops._qp(64, 4), "act": hip.MI_ACT_SWIGLU})
+    assert torch.equal(poisoned, sw)
     for sl in (slice(0, 256), slice(N - 256, N)):
         gw = oracle.quantized_matmul(x, *(a[sl] for a in q1), 64, 4, "bfloat16")
         uw = oracle.quantized_matmul(x, *(a[sl] for a in q3), 64, 4, "bfloat16")
