@@ -964,13 +964,15 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
             {  // (the host launches these with wk = 4)
                 // The four partial tiles reduced by all four waves. Quarter q of
                 // a tile is acc[.][.][4q .. 4q+3] (features 8q + 4h .. +3 of each
-                // 32x32 tile); every wave leaves its quarters in LDS as 16-byte
-                // words, QPR quarters per round (as many as the slots hold), and
-                // wave q adds the four copies of quarter q, ((p0 + p1) + p2) + p3
-                // -- the sums of a one-wave reduction -- into the registers of
-                // its own quarter 0 (handed over in the first round), then runs
-                // the epilogue for quarter q. Each wave thus reads a quarter of
-                // the partials and runs a quarter of the epilogue.
+                // 32x32 tile); every wave leaves the quarters it does not own in
+                // LDS as 16-byte words, QPR quarters per round (as many as the
+                // slots hold), and wave q adds the four copies of quarter q, its
+                // own from its registers, ((p0 + p1) + p2) + p3 -- the sums of a
+                // one-wave reduction -- into the registers of its own quarter 0
+                // (handed over in the first round), then runs the epilogue for
+                // quarter q. Each wave thus moves three quarters of its partials
+                // through LDS, reads three quarters of a tile and runs a quarter
+                // of the epilogue.
                 constexpr int AC = A * C;
                 constexpr int QPR = 4 * 4 * AC * 1024 <= Sh::LDS   ? 4
                                     : 4 * 2 * AC * 1024 <= Sh::LDS ? 2
@@ -982,7 +984,8 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
                 for (int q0 = 0; q0 < 4; q0 += QPR) {
                     if (q0 > 0) __syncthreads();  // the previous round's readers are done
 #pragma unroll
-                    for (int k = 0; k < QPR; ++k)
+                    for (int k = 0; k < QPR; ++k) {
+                        if (kw == q0 + k) continue;  // (wave-uniform) its own quarter stays
 #pragma unroll
                         for (int a = 0; a < A; ++a)
 #pragma unroll
@@ -992,18 +995,24 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
                                     make_float4(acc[a][c][4 * q], acc[a][c][4 * q + 1],
                                                 acc[a][c][4 * q + 2], acc[a][c][4 * q + 3]);
                             }
+                    }
                     __syncthreads();
 #pragma unroll
                     for (int k = 0; k < QPR; ++k) {
-                        if (kw != q0 + k) continue;  // wave-uniform
+                        if (kw != q0 + k) continue;  // wave-uniform: here kw == q0 + k
 #pragma unroll
                         for (int a = 0; a < A; ++a)
 #pragma unroll
                             for (int c = 0; c < C; ++c) {
+                                const int q = q0 + k;
                                 const float4 *bp = red + (k * AC + a * C + c) * 64 + lane;
                                 const int ws = QPR * AC * 64;  // one wave's words
-                                float4 v = bp[0];
-                                const float4 v1 = bp[ws], v2 = bp[2 * ws], v3 = bp[3 * ws];
+                                const float4 own = make_float4(acc[a][c][4 * q], acc[a][c][4 * q + 1],
+                                                               acc[a][c][4 * q + 2], acc[a][c][4 * q + 3]);
+                                float4 v = q == 0 ? own : bp[0];
+                                const float4 v1 = q == 1 ? own : bp[ws];
+                                const float4 v2 = q == 2 ? own : bp[2 * ws];
+                                const float4 v3 = q == 3 ? own : bp[3 * ws];
                                 v.x += v1.x;
                                 v.y += v1.y;
                                 v.z += v1.z;
