@@ -131,45 +131,57 @@ __global__ __launch_bounds__(256) void rms_row_kernel(const T *__restrict__ x,
 }
 
 // [qmm, add, rms_norm] after a K-part launch: row m of h is
-// T(resid + T(sum of the ks fp32 parts, in part order)), the [qmm, add]
+// T(resid + T(sum of the KS fp32 parts, in part order)), the [qmm, add]
 // epilogue, and the normalized row is rms_row_kernel's on that h (the same
-// chunks per thread, so the same sums). One workgroup per row.
-template <typename T>
-__global__ __launch_bounds__(256) void rms_parts_kernel(const float *__restrict__ part, int ks,
+// chunks per thread, so the same sums). One workgroup per row. Every load of
+// a thread (its chunks of each part, the residual and the weight) is issued
+// before the first add: a loop over a run-time part count had waited for each
+// part's loads in turn, one memory round trip per part and chunk.
+template <typename T, int KS>
+__global__ __launch_bounds__(256) void rms_parts_kernel(const float *__restrict__ part,
                                                         const T *__restrict__ resid,
                                                         const T *__restrict__ w,
                                                         T *__restrict__ h, T *__restrict__ y,
                                                         int64_t M, int64_t D, float eps) {
     const int64_t row = blockIdx.x;
     const int nc = (int)(D / 8);
-    uint4 xv[RMS_RC], wv[RMS_RC];
+    uint4 xv[RMS_RC], wv[RMS_RC], rv[RMS_RC];
+    float4 pv[RMS_RC][KS][2];
 #pragma unroll
     for (int i = 0; i < RMS_RC; ++i) {
         const int c = threadIdx.x + 256 * i;
         const int cc = c < nc ? c : nc - 1;  // clamped: in bounds, unused past nc
         const int64_t o = row * D + 8 * cc;
+#pragma unroll
+        for (int z = 0; z < KS; ++z) {
+            pv[i][z][0] = *(const float4 *)(part + z * M * D + o);
+            pv[i][z][1] = *(const float4 *)(part + z * M * D + o + 4);
+        }
+        rv[i] = ld16(resid + o);
         wv[i] = ld16(w + 8 * cc);
-        const uint4 rv = ld16(resid + o);
-        float4 lo = *(const float4 *)(part + o), hi = *(const float4 *)(part + o + 4);
+    }
+#pragma unroll
+    for (int i = 0; i < RMS_RC; ++i) {
+        const int c = threadIdx.x + 256 * i;
+        const float4 lo = pv[i][0][0], hi = pv[i][0][1];
         float s[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-        for (int z = 1; z < ks; ++z) {
-            lo = *(const float4 *)(part + z * M * D + o);
-            hi = *(const float4 *)(part + z * M * D + o + 4);
-            s[0] += lo.x;
-            s[1] += lo.y;
-            s[2] += lo.z;
-            s[3] += lo.w;
-            s[4] += hi.x;
-            s[5] += hi.y;
-            s[6] += hi.z;
-            s[7] += hi.w;
+#pragma unroll
+        for (int z = 1; z < KS; ++z) {
+            s[0] += pv[i][z][0].x;
+            s[1] += pv[i][z][0].y;
+            s[2] += pv[i][z][0].z;
+            s[3] += pv[i][z][0].w;
+            s[4] += pv[i][z][1].x;
+            s[5] += pv[i][z][1].y;
+            s[6] += pv[i][z][1].z;
+            s[7] += pv[i][z][1].w;
         }
         float f[8];
-        unpack8<T>(rv, f);
+        unpack8<T>(rv[i], f);
 #pragma unroll
         for (int e = 0; e < 8; ++e) f[e] = f[e] + (float)cvt<T>(s[e]);
         xv[i] = pack8<T>(f);
-        if (c < nc) st16(h + o, xv[i]);
+        if (c < nc) st16(h + row * D + 8 * c, xv[i]);
     }
     rms_row_store<T>(xv, wv, y + row * D, nc, D, eps);
 }
@@ -395,14 +407,21 @@ extern "C" int mi_qmm_affine_residual_rmsnorm_ws(const void *x, const uint32_t *
         return e;
     const int ks = (int)(need / (M * N * (int64_t)sizeof(float)));
     hipStream_t st = as_stream(stream);
-    if (dtype == MI_BF16)
-        rms_parts_kernel<bf16><<<(unsigned)M, 256, 0, st>>>(
-            (const float *)workspace, ks, (const bf16 *)resid, (const bf16 *)norm_w, (bf16 *)h,
-            (bf16 *)y, M, N, eps);
+#define MI_RMS_PARTS(TT, KS)                                                                   \
+    rms_parts_kernel<TT, KS><<<(unsigned)M, 256, 0, st>>>((const float *)workspace,              \
+                                                          (const TT *)resid, (const TT *)norm_w, \
+                                                          (TT *)h, (TT *)y, M, N, eps)
+    if (ks == 2 && dtype == MI_BF16)
+        MI_RMS_PARTS(bf16, 2);
+    else if (ks == 2)
+        MI_RMS_PARTS(f16, 2);
+    else if (ks == 4 && dtype == MI_BF16)
+        MI_RMS_PARTS(bf16, 4);
+    else if (ks == 4)
+        MI_RMS_PARTS(f16, 4);
     else
-        rms_parts_kernel<f16><<<(unsigned)M, 256, 0, st>>>(
-            (const float *)workspace, ks, (const f16 *)resid, (const f16 *)norm_w, (f16 *)h,
-            (f16 *)y, M, N, eps);
+        return fail(MI_ERR_UNSUPPORTED, "%d K parts", ks);
+#undef MI_RMS_PARTS
     return launch_status("qmm + residual + rms_norm (sum of K parts)");
 }
 

@@ -1553,27 +1553,43 @@ int launch_parts(const QParams &p, hipStream_t st) {
     return launch_mfma_cfg<T, BITS, 1, 1, EPI_STORE, KM_PART>(p, wk, st);
 }
 
-// Adds the K parts of p.part in part order and applies the single-part
-// epilogue EPI; thread t owns outputs 4t .. 4t + 3 (Nout % 4 == 0).
-template <typename T, int EPI>
+// Adds the KS K parts of p.part in part order and applies the single-part
+// epilogue EPI (EPI_STORE or EPI_RESID); thread t owns outputs 4t .. 4t + 3
+// (Nout % 4 == 0, so a thread's four outputs lie in one row). Every load (the
+// parts and the residual) is issued before the first add: a loop over a
+// run-time part count had waited for each part's loads in turn.
+template <typename T, int EPI, int KS>
 __global__ __launch_bounds__(256) void qmm_parts_sum_kernel(QParams p) {
+    static_assert(EPI == EPI_STORE || EPI == EPI_RESID, "single-part epilogues");
     const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t size = p.M * p.Nout;
     if (4 * q >= size) return;
-    // 32-bit row split: M * Nout < 2^31 (qmm_parts_bytes)
-    const int64_t o = 4 * q, m = (unsigned)o / (unsigned)p.Nout, n = o - m * p.Nout;
-    float4 v = *(const float4 *)(p.part + o);
-    float s[1][4] = {{v.x, v.y, v.z, v.w}};
-    for (int z = 1; z < p.ks; ++z) {
-        v = *(const float4 *)(p.part + z * size + o);
-        s[0][0] += v.x;
-        s[0][1] += v.y;
-        s[0][2] += v.z;
-        s[0][3] += v.w;
+    const int64_t o = 4 * q;
+    float4 v[KS];
+#pragma unroll
+    for (int z = 0; z < KS; ++z) v[z] = *(const float4 *)(p.part + z * size + o);
+    uint2 rr = {0, 0};
+    if constexpr (EPI == EPI_RESID) rr = ld8((const T *)p.resid + o);
+    float s[4] = {v[0].x, v[0].y, v[0].z, v[0].w};
+#pragma unroll
+    for (int z = 1; z < KS; ++z) {
+        s[0] += v[z].x;
+        s[1] += v[z].y;
+        s[2] += v[z].z;
+        s[3] += v[z].w;
     }
-    int64_t nb = 0;
-    const Bound bd = bind<EPI>(p, nb);
-    epi4<T, EPI, 1>(p, bd, m, n, s);
+    // the [qmm] / [qmm, add] epilogue of epi4 on a whole 4-output group
+    float y[4];
+    if constexpr (EPI == EPI_RESID) {
+        typedef typename Vec<T>::x4 V4;
+        const V4 rv = __builtin_bit_cast(V4, rr);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = (float)rv[e] + (float)cvt<T>(s[e]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = s[e];
+    }
+    st8((T *)p.y0 + o, pack4<T>(y));
 }
 
 template <int EPI>
@@ -1672,10 +1688,17 @@ int run_ws(QParams p, int bits, int dtype, void *ws, int64_t ws_bytes, void *str
     p.ks = kpart_count(p.M, p.K);
     p.part = (float *)ws;
     const unsigned blocks = (unsigned)ceil_div(p.M * p.Nout / 4, 256);
-    if (dtype == MI_BF16)
-        qmm_parts_sum_kernel<bf16, EPI><<<blocks, 256, 0, as_stream(stream)>>>(p);
+    hipStream_t st = as_stream(stream);
+    if (p.ks == 2 && dtype == MI_BF16)
+        qmm_parts_sum_kernel<bf16, EPI, 2><<<blocks, 256, 0, st>>>(p);
+    else if (p.ks == 2)
+        qmm_parts_sum_kernel<f16, EPI, 2><<<blocks, 256, 0, st>>>(p);
+    else if (p.ks == 4 && dtype == MI_BF16)
+        qmm_parts_sum_kernel<bf16, EPI, 4><<<blocks, 256, 0, st>>>(p);
+    else if (p.ks == 4)
+        qmm_parts_sum_kernel<f16, EPI, 4><<<blocks, 256, 0, st>>>(p);
     else
-        qmm_parts_sum_kernel<f16, EPI><<<blocks, 256, 0, as_stream(stream)>>>(p);
+        return fail(MI_ERR_UNSUPPORTED, "%d K parts", p.ks);
     return launch_status("quantized matmul (sum of K parts)");
 }
 
