@@ -144,7 +144,7 @@ def dominant_kernel(model, torch, ops):
         traffic = int(found.group(1)) if found else None
     return {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFS, "unit": "TFLOP/s",
             "frac": round(tf / BF16_PEAK_TFS, 4), "traffic": traffic,
-            "kernel": "qmm_mfma_mixed_kernel (dual gate/up + swiglu epilogue, mixed 128/64-token tiles)",
+            "kernel": "qmm_mfma_mixed3_kernel (dual gate/up + swiglu epilogue, 128/64/32-token tiles)",
             "shape": f"M={PROMPT} N=2x{N} K={K} 4-bit g64", "avg_us": round(us, 2),
             "flops_per_launch": fl}
 
