@@ -336,6 +336,19 @@ template <> struct Magic<f16> {
     }
 };
 
+// ((w >> 4j) & 0x000F000F) | Mg::pair -- the magic pair of nibbles j and
+// j + 4 of w -- in fewer instructions: the even and odd nibbles as bytes
+// (lo, hi) once per word, then one byte permute per pair that interleaves two
+// of those bytes with the magic exponent byte. Same bits.
+template <typename T>
+__device__ __forceinline__ uint32_t magic_pair(uint32_t w, int j) {
+    constexpr uint32_t e = (Magic<T>::pair >> 8) & 0xFFu;  // the exponent byte (0x43 / 0x64)
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    // v_perm_b32 bytes: 0..3 from the second operand, 4..7 from the first
+    const uint32_t sel = (j & 2) ? 0x04030401u : 0x04020400u;
+    return __builtin_amdgcn_perm(e * 0x01010101u, (j & 1) ? hi : lo, sel);
+}
+
 constexpr int QV_BATCH = 8;  // 16-byte weight chunks in flight per lane
 
 inline int64_t qmv_dot2_lds_bytes(int mr, int64_t K) { return mr * K * 2 + mr * (K / 32) * 4; }
@@ -461,7 +474,7 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
                 for (int wi = 0; wi < 4; ++wi)
 #pragma unroll
                     for (int jj = 0; jj < 4; ++jj)
-                        qp[wi][jj] = ((wd[wi] >> (4 * jj)) & 0x000F000Fu) | Mg::pair;
+                        qp[wi][jj] = magic_pair<T>(wd[wi], jj);
                 const float s = (float)sv[q][i];
                 const float bb = __builtin_fmaf(-Mg::value, s, (float)bv[q][i]);
 #pragma unroll
