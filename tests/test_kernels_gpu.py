@@ -225,6 +225,7 @@ def _kparts_call(name, *args):
     (128, 2560, 9728, 4, "bfloat16"),   # down_proj: 4 parts of 9 or 10 stages
     (100, 200, 4096, 8, "bfloat16"),    # ragged M and N, 8-bit
     (40, 512, 8192, 4, "float16"),      # 64-token part tiles
+    (72, 520, 4096, 4, "float16"),      # fp16 with 2 parts, ragged M
     (16, 256, 4224, 4, "bfloat16"),     # 66 stages, two waves a part: chunks of 16 / 17
 ])
 def test_qmm_k_parts_workspace_equals_one_launch(M, N, K, bits, dtype):
