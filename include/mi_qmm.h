@@ -101,7 +101,7 @@ int mi_qmm_affine_residual_rmsnorm(const void *x, const uint32_t *w, const void 
                                    int dtype, void *stream);
 
 /* K parts. On the MFMA path (16-bit T, 8 < M <= 128, K >= 4096) the
- * accumulation over K is cut into 2 (K < 8192) or 4 parts, each split over
+ * accumulation over K is cut into 4 parts, each split over
  * four waves of a workgroup, and the parts are added in order -- one fixed
  * order per (M, K), whichever entry point or tile computes the output.
  * Without a workspace a workgroup runs the parts in turn. The _ws entries run

@@ -411,11 +411,7 @@ extern "C" int mi_qmm_affine_residual_rmsnorm_ws(const void *x, const uint32_t *
     rms_parts_kernel<TT, KS><<<(unsigned)M, 256, 0, st>>>((const float *)workspace,              \
                                                           (const TT *)resid, (const TT *)norm_w, \
                                                           (TT *)h, (TT *)y, M, N, eps)
-    if (ks == 2 && dtype == MI_BF16)
-        MI_RMS_PARTS(bf16, 2);
-    else if (ks == 2)
-        MI_RMS_PARTS(f16, 2);
-    else if (ks == 4 && dtype == MI_BF16)
+    if (ks == 4 && dtype == MI_BF16)
         MI_RMS_PARTS(bf16, 4);
     else if (ks == 4)
         MI_RMS_PARTS(f16, 4);

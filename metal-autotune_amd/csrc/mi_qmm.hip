@@ -71,10 +71,12 @@ struct QParams {
 // each wave streaming 16-38 stages one after another. With a workspace the
 // parts run as workgroups of their own (grid z) and a second kernel adds them
 // in part order; without one a workgroup runs its parts in turn (qmm_mfma_tile)
-// and the sums are the same.
+// and the sums are the same. Four parts for both shapes (measured in the
+// Qwen3 prefill step: o_proj with 4 parts of 64-feature tiles beats 2 parts of
+// 32-feature tiles; down_proj with 8 parts loses 6 us a layer).
+constexpr int KPARTS = 4;
 inline int kpart_count(int64_t M, int64_t K) {
-    if (M <= 8 || M > 128 || K < 4096) return 1;
-    return K >= 8192 ? 4 : 2;
+    return (M <= 8 || M > 128 || K < 4096) ? 1 : KPARTS;
 }
 
 template <typename T> __device__ __forceinline__ float swiglu1(float g, float u) {
@@ -690,7 +692,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
     int64_t n_wave = n_blk;
     const Bound bd = bind<EPI>(p, n_wave);
     const int wk = p.wk;
-    // chunks = ks * wk is a power of two (ks, wk in {1, 2, 4}): chunk
+    // chunks = ks * wk is a power of two (ks in {1, 4}, wk in {1, 2, 4}): chunk
     // boundaries are a shift, not a division
     const int chunks = (KM == KM_ONE ? 1 : p.ks) * wk, nstages = (int)(K / XK);
     const int cshift = __builtin_ctz((unsigned)chunks);
@@ -1702,14 +1704,10 @@ int run_ws(QParams p, int bits, int dtype, void *ws, int64_t ws_bytes, void *str
     p.part = (float *)ws;
     const unsigned blocks = (unsigned)ceil_div(p.M * p.Nout / 4, 256);
     hipStream_t st = as_stream(stream);
-    if (p.ks == 2 && dtype == MI_BF16)
-        qmm_parts_sum_kernel<bf16, EPI, 2><<<blocks, 256, 0, st>>>(p);
-    else if (p.ks == 2)
-        qmm_parts_sum_kernel<f16, EPI, 2><<<blocks, 256, 0, st>>>(p);
-    else if (p.ks == 4 && dtype == MI_BF16)
-        qmm_parts_sum_kernel<bf16, EPI, 4><<<blocks, 256, 0, st>>>(p);
-    else if (p.ks == 4)
-        qmm_parts_sum_kernel<f16, EPI, 4><<<blocks, 256, 0, st>>>(p);
+    if (p.ks == KPARTS && dtype == MI_BF16)
+        qmm_parts_sum_kernel<bf16, EPI, KPARTS><<<blocks, 256, 0, st>>>(p);
+    else if (p.ks == KPARTS)
+        qmm_parts_sum_kernel<f16, EPI, KPARTS><<<blocks, 256, 0, st>>>(p);
     else
         return fail(MI_ERR_UNSUPPORTED, "%d K parts", p.ks);
     return launch_status("quantized matmul (sum of K parts)");

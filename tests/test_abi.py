@@ -75,12 +75,12 @@ def test_argmax_workspace_query_needs_no_device(lib):
 
 
 def test_qmm_workspace_query_needs_no_device(lib):
-    """K parts: 2 (K < 8192) or 4 fp32 copies of the output for 16-bit
-    8 < M <= 128, K >= 4096; 0 (one K part) elsewhere."""
+    """K parts: 4 fp32 copies of the output for 16-bit 8 < M <= 128,
+    K >= 4096; 0 (one K part) elsewhere."""
     lib.mi_qmm_workspace_bytes.restype = ctypes.c_int64
     I64, I = ctypes.c_int64, ctypes.c_int
     lib.mi_qmm_workspace_bytes.argtypes = [I64, I64, I64, I, I, I]
-    assert lib.mi_qmm_workspace_bytes(128, 2560, 4096, 64, 4, 2) == 2 * 128 * 2560 * 4
+    assert lib.mi_qmm_workspace_bytes(128, 2560, 4096, 64, 4, 2) == 4 * 128 * 2560 * 4
     assert lib.mi_qmm_workspace_bytes(128, 2560, 9728, 64, 4, 1) == 4 * 128 * 2560 * 4
     assert lib.mi_qmm_workspace_bytes(128, 2560, 4096, 64, 4, 0) == 0
     assert lib.mi_qmm_workspace_bytes(8, 2560, 4096, 64, 4, 2) == 0

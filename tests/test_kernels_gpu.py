@@ -221,12 +221,12 @@ def _kparts_call(name, *args):
 
 
 @pytest.mark.parametrize("M,N,K,bits,dtype", [
-    (128, 2560, 4096, 4, "bfloat16"),   # o_proj: 2 K parts
+    (128, 2560, 4096, 4, "bfloat16"),   # o_proj: 4 K parts of 4 stages
     (128, 2560, 9728, 4, "bfloat16"),   # down_proj: 4 parts of 9 or 10 stages
     (100, 200, 4096, 8, "bfloat16"),    # ragged M and N, 8-bit
     (40, 512, 8192, 4, "float16"),      # 64-token part tiles
-    (72, 520, 4096, 4, "float16"),      # fp16 with 2 parts, ragged M
-    (16, 256, 4224, 4, "bfloat16"),     # 66 stages, two waves a part: chunks of 16 / 17
+    (72, 520, 4096, 4, "float16"),      # fp16 with 4 parts, ragged M
+    (16, 256, 4224, 4, "bfloat16"),     # 66 stages, two waves a part: chunks of 8 / 9
 ])
 def test_qmm_k_parts_workspace_equals_one_launch(M, N, K, bits, dtype):
     """At shapes with K parts the _ws entries (the parts as workgroups of their
@@ -244,8 +244,7 @@ def test_qmm_k_parts_workspace_equals_one_launch(M, N, K, bits, dtype):
     xd, rd, nwd = to_torch(x, dtype), to_torch(res, dtype), to_torch(nw, dtype)
     w, s, b = _dev(*q, dtype)
     nbytes = L.mi_qmm_workspace_bytes(M, N, K, 64, bits, dt)
-    parts = 2 if K < 8192 else 4
-    assert nbytes == parts * M * N * 4
+    assert nbytes == 4 * M * N * 4  # four K parts
     ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device="cuda")  # NaN partials
     P = hip._ptr
     ys = {}
@@ -287,7 +286,7 @@ def test_qmm_k_parts_workspace_size():
     the 16-bit MFMA path; N must be a multiple of 4."""
     L = hip.lib()
     bf = hip._DT[torch.bfloat16]
-    assert L.mi_qmm_workspace_bytes(128, 2560, 4096, 64, 4, bf) == 2 * 128 * 2560 * 4
+    assert L.mi_qmm_workspace_bytes(128, 2560, 4096, 64, 4, bf) == 4 * 128 * 2560 * 4
     assert L.mi_qmm_workspace_bytes(128, 2560, 9728, 64, 4, bf) == 4 * 128 * 2560 * 4
     assert L.mi_qmm_workspace_bytes(9, 64, 8192, 64, 8, bf) == 4 * 9 * 64 * 4
     for M, N, K, dt in ((8, 2560, 4096, bf), (129, 2560, 4096, bf), (128, 9728, 2560, bf),
