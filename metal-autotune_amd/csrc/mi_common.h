@@ -61,6 +61,14 @@ template <typename T> __device__ __forceinline__ uint32_t pk2(float a, float b) 
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((F2){a, b}, T2));
 }
 
+// Unpack the 4 values of an 8-byte group of T into floats.
+template <typename T> __device__ __forceinline__ void unpack4(uint2 raw, float (&f)[4]) {
+    typedef typename Vec<T>::x4 V;
+    V v = __builtin_bit_cast(V, raw);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = (float)v[i];
+}
+
 template <typename T> __device__ __forceinline__ uint2 pack4(const float (&f)[4]) {
     typedef typename Vec<T>::x4 V;
     V v;

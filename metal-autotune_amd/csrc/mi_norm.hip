@@ -235,7 +235,12 @@ __device__ __forceinline__ float rope_second(float a, float c, float cs, float s
     return __builtin_fmaf(a, sn, c * cs);
 }
 
-template <typename T, int R>
+// R lanes per row. VEC (16-bit T, D == 8 R, every row 16-byte aligned): each
+// lane owns four rotation pairs (elements 4t..4t+3 and their partners D/2
+// on), moved as 8-byte loads and stores, or eight consecutive elements of a
+// row that is only normalized or copied; otherwise R = D / 2 and a lane owns
+// one pair (or the general loop runs).
+template <typename T, int R, bool VEC>
 __global__ __launch_bounds__(256) void norm_rope_kernel(NRJobs jobs, int64_t B, int64_t L,
                                                         int64_t D, float eps, int trad,
                                                         float log2base, float scale,
@@ -262,7 +267,75 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NRJobs jobs, int64_t B, 
     const int half = dims / 2;
     const int slots = (int)(D / 2);
     const float position = (float)(l + offset) * scale;
-    if (!trad && D == 2 * R && dims == D) {
+    if constexpr (VEC) {
+        if (!trad && dims == D) {
+            // four pairs per lane: one sum of squares over the lane's eight
+            // elements, a butterfly over the row's R lanes, the same
+            // normalization and rotation per element as below
+            const int e0 = 4 * t, hd = (int)(D / 2);
+            const uint2 xa = ld8(xr + e0), xc = ld8(xr + hd + e0);
+            const uint2 wa = w ? ld8(w + e0) : make_uint2(0, 0);
+            const uint2 wc = w ? ld8(w + hd + e0) : make_uint2(0, 0);
+            float sn[4], cs[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float inv_freq = exp2f(-(float)(2 * (e0 + e)) / (float)dims * log2base);
+                sincosf(position * inv_freq, &sn[e], &cs[e]);
+            }
+            float a[4], c[4];
+            unpack4<T>(xa, a);
+            unpack4<T>(xc, c);
+            if (w) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ss = __builtin_fmaf(a[e], a[e], ss);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ss = __builtin_fmaf(c[e], c[e], ss);
+#pragma unroll
+                for (int o = R / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, R);
+                const float inv = 1.0f / __fsqrt_rn(ss / (float)D + eps);
+                float ga[4], gc[4];
+                unpack4<T>(wa, ga);
+                unpack4<T>(wc, gc);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    a[e] = (float)cvt<T>(ga[e] * (float)cvt<T>(a[e] * inv));
+                    c[e] = (float)cvt<T>(gc[e] * (float)cvt<T>(c[e] * inv));
+                }
+            }
+            float r0[4], r1[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                r0[e] = rope_first(a[e], c[e], cs[e], sn[e]);
+                r1[e] = rope_second(a[e], c[e], cs[e], sn[e]);
+            }
+            st8(orow + e0, pack4<T>(r0));
+            st8(orow + hd + e0, pack4<T>(r1));
+            return;
+        }
+        if (dims == 0) {  // no rotation: the normalized row, or a plain copy
+            const uint4 xv = ld16(xr + 8 * t);
+            if (!w) {
+                st16(orow + 8 * t, xv);
+                return;
+            }
+            const uint4 wv = ld16(w + 8 * t);
+            float f[8], g[8];
+            unpack8<T>(xv, f);
+            unpack8<T>(wv, g);
+            float ss = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(f[e], f[e], ss);
+#pragma unroll
+            for (int o = R / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, R);
+            const float inv = 1.0f / __fsqrt_rn(ss / (float)D + eps);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = (float)cvt<T>(g[e] * (float)cvt<T>(f[e] * inv));
+            st16(orow + 8 * t, pack8<T>(f));
+            return;
+        }
+    }
+    if (!VEC && !trad && D == 2 * R && dims == D) {
         // Each lane owns elements t and t + R: its two terms of the RMS and
         // one rotation pair. One load of each, issued with the weights before
         // the angle math, which then runs under their latency; the same
@@ -334,17 +407,37 @@ int launch_norm_rope(const NRJobs &jobs, int64_t B, int64_t L, int64_t D, float 
     if (rows >= ((int64_t)1 << 31))  // the kernel splits a row index in 32 bits
         return fail(MI_ERR_UNSUPPORTED, "norm_rope of %lld rows", (long long)rows);
     const int64_t slots = D / 2;
-#define MI_NR_LAUNCH(RR)                                                                       \
-    norm_rope_kernel<T, RR><<<(unsigned)ceil_div(rows, 256 / RR), 256, 0, st>>>(                \
+#define MI_NR_LAUNCH(RR, V)                                                                    \
+    norm_rope_kernel<T, RR, V><<<(unsigned)ceil_div(rows, 256 / RR), 256, 0, st>>>(             \
         jobs, B, L, D, eps, trad, log2base, scale, offset)
+    // 16-byte rows: every job's x, weight and output base 16-byte aligned and
+    // its x row stride a multiple of 8 elements (D itself is)
+    auto row16 = [&](const NRJob &j) {
+        return aligned(j.x, 16) && aligned(j.w, 16) && aligned(j.out, 16) && j.xs % 8 == 0;
+    };
+    if constexpr (sizeof(T) == 2) {
+        const bool vec = D >= 64 && D <= 512 && (D & (D - 1)) == 0 && row16(jobs.j0) &&
+                         row16(jobs.j1) && row16(jobs.j2);
+        if (vec) {
+            if (D == 512)
+                MI_NR_LAUNCH(64, true);
+            else if (D == 256)
+                MI_NR_LAUNCH(32, true);
+            else if (D == 128)
+                MI_NR_LAUNCH(16, true);
+            else
+                MI_NR_LAUNCH(8, true);
+            return launch_status("norm_rope");
+        }
+    }
     if (slots >= 64)
-        MI_NR_LAUNCH(64);
+        MI_NR_LAUNCH(64, false);
     else if (slots >= 32)
-        MI_NR_LAUNCH(32);
+        MI_NR_LAUNCH(32, false);
     else if (slots >= 16)
-        MI_NR_LAUNCH(16);
+        MI_NR_LAUNCH(16, false);
     else
-        MI_NR_LAUNCH(8);
+        MI_NR_LAUNCH(8, false);
 #undef MI_NR_LAUNCH
     return launch_status("norm_rope");
 }
