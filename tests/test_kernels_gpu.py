@@ -473,6 +473,40 @@ def test_norm_rope(H, D, L, offset, norm):
     _close(got, want, "bfloat16")
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_norm_rope_norm_only(D):
+    """rope dims 0 with a norm weight: the q/k RMSNorm alone (16-byte rows:
+    eight consecutive elements per lane)."""
+    r = rng(905 + D)
+    H, L = 8, 9
+    x = oracle.round_to(r.normal(0, 1, (1, L, H * D)), "bfloat16")
+    w = oracle.round_to(1 + 0.2 * r.normal(0, 1, D), "bfloat16")
+    got = ops.norm_rope(to_torch(x, "bfloat16"), to_torch(w, "bfloat16"), H, 1e-6, 0, 1e6, 0)
+    _close(got, oracle.norm_rope(x, w, 1e-6, H, 0, 1e6, 0, "bfloat16"), "bfloat16")
+
+
+@pytest.mark.parametrize("dims", [128, 0])
+def test_norm_rope_unaligned_rows(dims):
+    """Rows whose stride is not a multiple of 8 elements take the one-pair-per-
+    lane form (and the general loop for dims 0); both stay within the oracle
+    bar, and within it of the 16-byte-row form on the same values."""
+    r = rng(915 + dims)
+    H, D, L, offset = 8, 128, 11, 3
+    x = oracle.round_to(r.normal(0, 1, (1, L, H * D)), "bfloat16")
+    w = oracle.round_to(1 + 0.2 * r.normal(0, 1, D), "bfloat16")
+    pad = torch.zeros((1, L, H * D + 4), dtype=torch.bfloat16, device="cuda")
+    pad[:, :, :H * D] = to_torch(x, "bfloat16")
+    wd = to_torch(w, "bfloat16")
+    out = torch.empty((1, H, L, D), dtype=torch.bfloat16, device="cuda")
+    hip._check(hip.lib().mi_norm_rope(
+        pad.data_ptr(), wd.data_ptr(), out.data_ptr(), 1, L, H, D, H * D + 4, 1e-6, dims, 0, 1e6,
+        1.0, offset, L, 0, hip._dt(pad), torch.cuda.current_stream().cuda_stream), "norm_rope")
+    want = oracle.norm_rope(x, w, 1e-6, H, dims, 1e6, offset, "bfloat16")
+    _close(out, want, "bfloat16")
+    vec = ops.norm_rope(to_torch(x, "bfloat16"), wd, H, 1e-6, dims, 1e6, offset)
+    _close(out, to_np(vec), "bfloat16")
+
+
 def test_rope_partial_traditional_fp32():
     r = rng(950)
     x = r.normal(0, 1, (2, 3, 9, 32)).astype(np.float32)
