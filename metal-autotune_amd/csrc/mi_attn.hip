@@ -316,20 +316,24 @@ __global__ __launch_bounds__(64 * ATT_STREAMS) void attn_split_kernel(
     }
 
     // Merge: every wave leaves its stream's (o, l, m) in LDS (over the V^T
-    // tiles); wave w then folds the four streams, in stream order, for O^T
-    // tile t = w (D = 64: tiles 0 and 1) and stores that tile. Each wave
-    // recomputes the same (m, l) chain, so the result is that of one wave
-    // folding every tile.
-    float *part = (float *)lds;
+    // tiles) as 16-byte words; wave w then folds the four streams, in stream
+    // order, for O^T tile t = w (D = 64: tiles 0 and 1) and stores that tile.
+    // Each wave recomputes the same (m, l) chain, so the result is that of one
+    // wave folding every tile.
+    // Layout of a wave's state: float4 [DT * 4][64] (accumulator registers
+    // 4j .. 4j + 3 of tile t at t * 4 + j), then float2 (l, m) [64].
+    float4 *part = (float4 *)lds;
+    constexpr int PART4 = L::PART_FLOATS / 4;  // one wave's state in float4
     __syncthreads();  // every wave is done with its V^T tile
     {
-        float *pp = part + (size_t)wave * L::PART_FLOATS;
+        float4 *pp = part + (size_t)wave * PART4;
 #pragma unroll
         for (int t = 0; t < DT; ++t)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) pp[(t * 16 + i) * 64 + lane] = st.o[t][i];
-        pp[DT * 16 * 64 + lane] = st.l;
-        pp[DT * 16 * 64 + 64 + lane] = st.m;
+            for (int j = 0; j < 4; ++j)
+                pp[(t * 4 + j) * 64 + lane] = make_float4(st.o[t][4 * j], st.o[t][4 * j + 1],
+                                                          st.o[t][4 * j + 2], st.o[t][4 * j + 3]);
+        ((float2 *)(pp + DT * 4 * 64))[lane] = make_float2(st.l, st.m);
     }
     __syncthreads();
     if (!qok) return;
@@ -338,16 +342,30 @@ __global__ __launch_bounds__(64 * ATT_STREAMS) void attn_split_kernel(
     for (int t = wave; t < DT; t += ATT_STREAMS) {  // wave-uniform
         f32x16 o;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[i] = part[(t * 16 + i) * 64 + lane];
-        float m = part[DT * 16 * 64 + 64 + lane], l = part[DT * 16 * 64 + lane];
+        for (int j = 0; j < 4; ++j) {
+            const float4 v = part[(t * 4 + j) * 64 + lane];
+            o[4 * j] = v.x;
+            o[4 * j + 1] = v.y;
+            o[4 * j + 2] = v.z;
+            o[4 * j + 3] = v.w;
+        }
+        const float2 lm = ((const float2 *)(part + DT * 4 * 64))[lane];
+        float l = lm.x, m = lm.y;
         for (int w = 1; w < ATT_STREAMS; ++w) {
-            const float *pp = part + (size_t)w * L::PART_FLOATS;
-            const float mw = pp[DT * 16 * 64 + 64 + lane];
+            const float4 *pp = part + (size_t)w * PART4;
+            const float2 lmw = ((const float2 *)(pp + DT * 4 * 64))[lane];
+            const float mw = lmw.y;
             if (mw == -INFINITY) continue;
             const MergeCoef c = merge_coef(m, mw);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) o[i] = merge_one(o[i], pp[(t * 16 + i) * 64 + lane], c);
-            l = merge_one(l, pp[DT * 16 * 64 + lane], c);
+            for (int j = 0; j < 4; ++j) {
+                const float4 v = pp[(t * 4 + j) * 64 + lane];
+                o[4 * j] = merge_one(o[4 * j], v.x, c);
+                o[4 * j + 1] = merge_one(o[4 * j + 1], v.y, c);
+                o[4 * j + 2] = merge_one(o[4 * j + 2], v.z, c);
+                o[4 * j + 3] = merge_one(o[4 * j + 3], v.w, c);
+            }
+            l = merge_one(l, lmw.x, c);
             m = c.m_new;
         }
         attn_store_tile<T>(o, l, orow, t, h2);
