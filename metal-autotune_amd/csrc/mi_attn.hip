@@ -261,11 +261,20 @@ __global__ __launch_bounds__(64 * ATT_STREAMS) void attn_split_kernel(
     const int64_t qrow = q0 + r;
     const bool qok = qrow < Lq;
 
-    uint4 qf[DS];
-    {
-        const T *qp = q + ((b * H + hq) * Lq + (qok ? qrow : 0)) * D + 8 * h2;
+    // The q block (32 rows x D) is read once per workgroup: each thread loads
+    // QPT of its 16-byte chunks (rows past Lq: zeros) and stores them to LDS,
+    // 16-byte chunk c of row rr at position c ^ (rr % (D / 8)), so the 32 rows'
+    // reads of one chunk hit distinct banks; after the barrier below every
+    // wave reads its MFMA fragments. (Each wave had loaded the whole block.)
+    constexpr int QCR = D / 8;         // 16-byte chunks per q row
+    constexpr int QPT = 32 * QCR / 256;  // chunks per thread
+    __shared__ uint4 qsh[32 * QCR];
+    uint4 qv[QPT];
 #pragma unroll
-        for (int s = 0; s < DS; ++s) qf[s] = qok ? ld16(qp + 16 * s) : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < QPT; ++i) {
+        const int c = (int)threadIdx.x + 256 * i, rr = c / QCR;
+        qv[i] = q0 + rr < Lq ? ld16(q + ((b * H + hq) * Lq + q0 + rr) * D + 8 * (c % QCR))
+                             : make_uint4(0, 0, 0, 0);
     }
     AttnState<D> st;
     attn_init(st);
@@ -288,7 +297,18 @@ __global__ __launch_bounds__(64 * ATT_STREAMS) void attn_split_kernel(
 #pragma unroll
         for (int i = 0; i < VCH; ++i) vreg[i] = ld16(vb + kc * D + (h2 + 2 * i) * 8);
     };
-    if (wave < ntiles) fetch(wave);
+    // every wave issues its first tile's loads (a wave past the last tile a
+    // clamped, unused one), so the wait for q below leaves them in flight
+    fetch(wave);
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+        const int c = (int)threadIdx.x + 256 * i, rr = c / QCR;
+        qsh[rr * QCR + ((c % QCR) ^ (rr % QCR))] = qv[i];
+    }
+    __syncthreads();
+    uint4 qf[DS];
+#pragma unroll
+    for (int s = 0; s < DS; ++s) qf[s] = qsh[r * QCR + ((2 * s + h2) ^ (r % QCR))];
 
     for (int kt = wave; kt < ntiles; kt += ATT_STREAMS) {  // wave-uniform
         // S^T and the softmax first: the V loads, issued after K's, land
