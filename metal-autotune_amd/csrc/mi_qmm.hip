@@ -735,15 +735,28 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
     // offset plus a stage offset stays below 2^32 since M * K * size < 2^31).
     const uint32_t xbytes = (uint32_t)(p.M * K * (int64_t)sizeof(T));
     const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(p.x, xbytes);
-    uint32_t xoff[Sh::XOPS];
+    // XREMAT: the 8-bit tiles with eight accumulators leave no registers for
+    // the XOPS offsets (held across the loop they spilled, and every reload
+    // before a DMA waited for all the DMAs in flight). Those tiles rebuild
+    // offset j per stage as xrow[j % 2] + j * 8 rows: row 8j + l/8 of lane l
+    // has swizzle ((4j + l/16) & 7), which depends on j only through j % 2.
+    // A token past M then lies at or past xbytes by its own offset (row * K *
+    // size >= M * K * size), which is the zero-returning case above; should
+    // that offset wrap past 2^32 it lands inside x's buffer instead, a valid
+    // read whose rows the epilogue never stores.
+    constexpr bool XREMAT = BITS == 8 && A * C >= 8;
+    uint32_t xoff[XREMAT ? 1 : Sh::XOPS], xrow[2];
 #pragma unroll
-    for (int j = 0; j < Sh::XOPS; ++j) {
+    for (int j = 0; j < (XREMAT ? 2 : Sh::XOPS); ++j) {
         const int row = 8 * j + (lane >> 3);
         const int chunk = (lane & 7) ^ ((row >> 1) & 7);
-        xoff[j] = m_blk + row < p.M
-                      ? (uint32_t)(((m_blk + row) * K + 8 * chunk) * (int64_t)sizeof(T))
-                      : xbytes;
+        const uint32_t o = (uint32_t)(((m_blk + row) * K + 8 * chunk) * (int64_t)sizeof(T));
+        if constexpr (XREMAT)
+            xrow[j] = o;
+        else
+            xoff[j] = m_blk + row < p.M ? o : xbytes;
     }
+    const uint32_t xrows8 = (uint32_t)(8 * K * (int64_t)sizeof(T));  // 8 token rows in bytes
     f32x16 acc[A][C];
     for (int kp = 0; kp < nparts; ++kp) {  // workgroup-uniform
         const int cix = (KM == KM_PART ? kz : kp) * wk + kw;
@@ -775,10 +788,22 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
         auto issue = [&](int st, char *slot) {
             const int k0 = kbeg + st * XK;
             const uint32_t xs = (uint32_t)k0 * sizeof(T);
+            if constexpr (XREMAT) {
+                // opaque per stage, so the offsets are not hoisted out of the loop
+                uint32_t r0 = xrow[0], r1 = xrow[1];
+                launder(r0);
+                launder(r1);
 #pragma unroll
-            for (int j = 0; j < Sh::XOPS; ++j)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(slot + j * 1024), 16, xoff[j], xs,
-                                                         0, 0);
+                for (int j = 0; j < Sh::XOPS; ++j)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        xr, (lds_ptr)(slot + j * 1024), 16, ((j & 1) ? r1 : r0) + (uint32_t)(j >> 1) * 2u * xrows8,
+                        xs, 0, 0);
+            } else {
+#pragma unroll
+                for (int j = 0; j < Sh::XOPS; ++j)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(slot + j * 1024), 16, xoff[j],
+                                                             xs, 0, 0);
+            }
             if constexpr (Sh::WREG) return;
 #pragma unroll
             for (int u = 0; u < SPS; ++u) {
@@ -1466,7 +1491,7 @@ int launch_mfma(const QParams &p, hipStream_t st) {
     // 64 < M <= 128 whose 64-token grid (2 nt workgroups) puts one workgroup
     // more on some CUs than on others: mixed tiles make it exactly two per CU,
     // at most one of the larger workgroups on each, when two of them fit a
-    // CU's LDS (4-bit; the 8-bit 128-token dual tile spills).
+    // CU's LDS (4-bit; measured only on the 4-bit Qwen3 shapes).
     // - more than two per CU (dual outputs): 128/64/32-token tiles while the
     //   feature tiles outnumber the CUs by at most a quarter, else 128/64;
     // - between one and one and a half per CU: 64/32-token tiles.

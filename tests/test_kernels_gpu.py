@@ -391,6 +391,38 @@ def test_qmm_dual_mixed_tiles_equal_plain_tiles(M, N):
         _close(sw[..., sl], oracle.swiglu(gw, uw, "bfloat16"), "bfloat16")
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_qmm_dual_8bit_large_tiles(dtype):
+    """The 8-bit dual from M = 512 runs 128-token tiles whose x offsets are
+    rebuilt per stage (M = 520: a last tile of 8 tokens, whose other 120 rows
+    read zeros past the end of x). Within tolerance of the oracle; rows
+    [0, 512) and [480, 520) equal, bit for bit, MFMA launches of M = 512 and
+    M = 40 (32-token tiles, the same K split; M <= 8 would take the GEMV,
+    whose factored sums round differently); every element written (NaN-filled
+    output); the fused SwiGLU equals swiglu of the unfused pair bit for bit."""
+    M, N, K = 520, 512, 1024
+    r = rng(790)
+    x = oracle.round_to(r.normal(0, 1, (1, M, K)), dtype)
+    q1 = _quant(791, N, K, bits=8, dtype=dtype)
+    q3 = _quant(792, N, K, bits=8, dtype=dtype)
+    xd = to_torch(x, dtype)
+    w = (*_dev(*q1, dtype), *_dev(*q3, dtype))
+    g, u = ops.qmm_dual(xd, *w, bits=8)
+    gw = oracle.quantized_matmul(x, *q1, 64, 8, dtype)
+    uw = oracle.quantized_matmul(x, *q3, 64, 8, dtype)
+    _close(g, gw, dtype)
+    _close(u, uw, dtype)
+    for lo, hi in ((0, 512), (480, 520)):
+        pg, pu = ops.qmm_dual(xd[:, lo:hi].contiguous(), *w, bits=8)
+        assert torch.equal(g[:, lo:hi], pg) and torch.equal(u[:, lo:hi], pu), (lo, hi)
+    sw = ops.qmm_dual(xd, *w, bits=8, swiglu=True)
+    assert torch.equal(sw, ops.swiglu(g, u))
+    _close(sw, oracle.swiglu(gw, uw, dtype), dtype)
+    poisoned = torch.full_like(sw, float("nan"))
+    hip.b_qmm_dual([xd, *w], [poisoned], {**ops._qp(64, 8), "act": hip.MI_ACT_SWIGLU})
+    assert torch.equal(poisoned, sw)
+
+
 @pytest.mark.parametrize("M", [1, 3, 8, 16, 40, 128, 300])
 @pytest.mark.parametrize("bits,dtype", [(4, "bfloat16"), (8, "float16"), (4, "float32")])
 def test_qmm_grouped3_equals_three_launches(M, bits, dtype):
