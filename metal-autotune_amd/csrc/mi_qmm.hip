@@ -145,10 +145,25 @@ __device__ __forceinline__ void epi1(const QParams &p, const Bound &bd, int64_t 
     }
 }
 
+// Whether epi4 takes its vector path at (m, n): in range, four whole features.
+__device__ __forceinline__ bool epi4_vec(const QParams &p, const Bound &bd, int64_t m, int64_t n) {
+    return m < p.M && n + 4 <= bd.Nout && !(bd.Nout & 3);
+}
+
+// EPI_RESID: the residual's four values at (m, n) for epi4's vector path,
+// loaded ahead so a wave's loads are all in flight before its first store
+// (each epi4 loading its own had waited for every load in turn); zeros where
+// the vector path does not run (the element path loads its own).
+template <typename T>
+__device__ __forceinline__ uint2 resid4(const QParams &p, const Bound &bd, int64_t m, int64_t n) {
+    return epi4_vec(p, bd, m, n) ? ld8((const T *)p.resid + m * bd.Nout + n) : make_uint2(0u, 0u);
+}
+
 // Epilogue for 4 consecutive output features n..n+3 of token m; acc[part][e].
+// rpre: EPI_RESID's residual from resid4 (null: loaded here).
 template <typename T, int EPI, int P>
 __device__ __forceinline__ void epi4(const QParams &p, const Bound &bd, int64_t m, int64_t n,
-                                     const float (&acc)[P][4]) {
+                                     const float (&acc)[P][4], const uint2 *rpre = nullptr) {
     if (m >= p.M || n >= bd.Nout) return;
     if (n + 4 > bd.Nout || (bd.Nout & 3)) {  // ragged tail: element stores
         for (int e = 0; e < 4 && n + e < bd.Nout; ++e) {
@@ -165,7 +180,7 @@ __device__ __forceinline__ void epi4(const QParams &p, const Bound &bd, int64_t 
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = acc[0][e];
     } else if constexpr (EPI == EPI_RESID) {
-        const uint2 rr = ld8((const T *)p.resid + o);
+        const uint2 rr = rpre ? *rpre : ld8((const T *)p.resid + o);
         typedef typename Vec<T>::x4 V4;
         const V4 rv = __builtin_bit_cast(V4, rr);
 #pragma unroll
@@ -1088,6 +1103,16 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
                         }
                     }
                 } else {
+                    // EPI_RESID: every residual load of the quarter first
+                    uint2 rres[EPI == EPI_RESID ? C : 1][EPI == EPI_RESID ? A : 1];
+                    if constexpr (EPI == EPI_RESID && P == 1) {
+#pragma unroll
+                        for (int c = 0; c < C; ++c)
+#pragma unroll
+                            for (int a = 0; a < A; ++a)
+                                rres[c][a] = resid4<T>(p, bd, m_blk + 32 * c + r,
+                                                       n_wave + 32 * a + 8 * blk + 4 * h);
+                    }
 #pragma unroll
                     for (int c = 0; c < C; ++c) {
                         const int64_t m = m_blk + 32 * c + r;
@@ -1096,7 +1121,9 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
                             for (int a = 0; a < A; ++a) {
                                 float v[1][4] = {{acc[a][c][0], acc[a][c][1], acc[a][c][2],
                                                   acc[a][c][3]}};
-                                epi4<T, EPI, 1>(p, bd, m, n_wave + 32 * a + 8 * blk + 4 * h, v);
+                                const uint2 *rp = nullptr;
+                                if constexpr (EPI == EPI_RESID) rp = &rres[c][a];
+                                epi4<T, EPI, 1>(p, bd, m, n_wave + 32 * a + 8 * blk + 4 * h, v, rp);
                             }
                         } else {
                             float v[P][4];

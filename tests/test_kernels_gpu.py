@@ -182,15 +182,20 @@ def test_qmm_rejects_bad_shapes():
 # ---------------------------------------------------------- region epilogues
 
 
-@pytest.mark.parametrize("M", [1, 16, 128])
-def test_qmm_residual(M):
-    r = rng(400 + M)
-    K, N = 2048, 512
+@pytest.mark.parametrize("M,N,bits", [(1, 512, 4), (16, 512, 4), (128, 512, 4), (520, 512, 4),
+                                       (520, 510, 4), (520, 512, 8)])
+def test_qmm_residual(M, N, bits):
+    """[qmm, add]. M = 520 runs 128-token tiles (a last tile of 8 tokens)
+    whose epilogue loads every residual of a wave before its first store;
+    N = 510 (not a multiple of 4) takes the element-wise epilogue."""
+    r = rng(400 + M + N + bits)
+    K = 2048
     x = oracle.round_to(r.normal(0, 1, (1, M, K)), "bfloat16")
     res = oracle.round_to(r.normal(0, 1, (1, M, N)), "bfloat16")
-    wq, s, b = _quant(15, N, K)
-    y = ops.qmm_residual(to_torch(x, "bfloat16"), *_dev(wq, s, b, "bfloat16"), to_torch(res, "bfloat16"))
-    t = oracle.quantized_matmul(x, wq, s, b, 64, 4, "bfloat16")
+    wq, s, b = _quant(15, N, K, bits=bits)
+    y = ops.qmm_residual(to_torch(x, "bfloat16"), *_dev(wq, s, b, "bfloat16"), to_torch(res, "bfloat16"),
+                         bits=bits)
+    t = oracle.quantized_matmul(x, wq, s, b, 64, bits, "bfloat16")
     _close(y, oracle.round_to(res.astype(np.float64) + t, "bfloat16"), "bfloat16")
 
 
