@@ -478,6 +478,9 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
         for (int m = 0; m < MR; ++m) acc[q][m] = 0.0f;
 
     for (int64_t base = j; base < cpr; base += 16 * QV_BATCH) {
+        // (Without PF the compiler sinks each chunk's loads to its use behind
+        // the `c >= cpr` exit, so a lane fetches its chunks one after another;
+        // at 58 registers eight waves per SIMD keep the loads in flight.)
         if (!PF || base != j) load_batch(base);
 #pragma unroll
         for (int i = 0; i < QV_BATCH; ++i) {
