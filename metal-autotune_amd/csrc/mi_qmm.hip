@@ -1505,9 +1505,11 @@ int launch_mfma(const QParams &p, hipStream_t st) {
     const int64_t nt = ceil_div(p.Nout, 32);
     const bool large = p.M >= 512 || nt * ceil_div(p.M, 64) > 2048;
     if constexpr (P == 1) {
-        // (8-bit: 32x128, whose stage slots still fit the LDS twice; the
-        // grouped q/k/v epilogue binds one part per 32-feature tile)
-        constexpr int AL = (BITS == 4 && EPI != EPI_GROUP3) ? 2 : 1;
+        // (both widths; the grouped q/k/v epilogue binds one part per
+        // 32-feature tile. 8-bit took 32x128 tiles while its 64x128 tile
+        // spilled; without the spill, LFM2's 8-bit out/down_proj at M = 2048
+        // went 84.9 -> 64.4 us on average)
+        constexpr int AL = EPI != EPI_GROUP3 ? 2 : 1;
         // wide single-part 4-bit outputs take 64x128 tiles from M = 128
         // (N = 9728: 23.1 -> 21.3 us; narrower N loses parallelism)
         const bool wide = AL == 2 && p.M >= 128 && nt >= 256;

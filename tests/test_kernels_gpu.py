@@ -131,7 +131,7 @@ def test_qmm_config2_shape(M):
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
 @pytest.mark.parametrize("bits,gs", [(4, 64), (8, 64), (4, 32), (4, 128), (8, 32)])
-@pytest.mark.parametrize("M", [1, 7, 40, 130])
+@pytest.mark.parametrize("M", [1, 7, 40, 130, 520])
 def test_qmm_dtypes_bits_groups(dtype, bits, gs, M):
     r = rng(300 + M + bits)
     K, N = 512, 200  # N not a multiple of 32: ragged output tiles
