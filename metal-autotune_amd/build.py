@@ -7,7 +7,8 @@ oracle/Makefile; `build_all()` runs both.
 
 Flags: -O3, gfx950 only, packed-fp32 VALU forms disabled on the device
 (`-packed-fp32-ops`); the host pass warns that it does not know the feature,
-which is harmless.
+which is harmless. SOURCE_FLAGS adds per-file flags (mi_attn.hip: MFMA
+results in arch VGPRs).
 """
 
 from __future__ import annotations
@@ -35,6 +36,15 @@ FLAGS = [
 ]
 
 
+# Per-source device flags. mi_attn.hip: MFMA results in arch VGPRs. By
+# default the compiler kept the attention accumulators in AGPRs and copied
+# them through VGPRs for every tile's softmax rescale and stream merge
+# (272 v_accvgpr_read/write in the 64-wide shared kernel, about 40 % of its
+# loop's VALU), which also cost occupancy. Same instructions otherwise, same
+# results.
+SOURCE_FLAGS = {"mi_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _run(cmd: list[str]) -> None:
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
@@ -52,7 +62,7 @@ def build_hip(jobs: int | None = None, verbose: bool = False) -> Path:
 
     def compile_one(pair):
         src, obj = pair
-        _run([HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)])
+        _run([HIPCC, *FLAGS, *SOURCE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)])
         if verbose:
             print(f"  compiled {src.name}", flush=True)
 
