@@ -457,45 +457,50 @@ __global__ __launch_bounds__(256) void attn_shared_kernel(
         const int s = kt % ATT_STREAMS + 1;
         return s < ATT_STREAMS && s < ntiles ? s : -1;
     };
-    AttnState<D> tot, cur;
+    // One pass per stream: its tiles in turn into cur, then cur folded into
+    // tot in stream order. (With the fold inside one loop over all tiles the
+    // compiler copied both states at every tile.)
+    AttnState<D> tot;
     attn_init(tot);
-    attn_init(cur);
     if (ntiles > 0) fetch(0);
-    for (int kt = ntiles > 0 ? 0 : -1; kt >= 0;) {  // workgroup-uniform
-        __syncthreads();  // every wave is done with the previous tile
+    const int nstreams = ntiles < ATT_STREAMS ? ntiles : ATT_STREAMS;
+    for (int sw = 0; sw < nstreams; ++sw) {  // workgroup-uniform
+        AttnState<D> cur;
+        attn_init(cur);
+        for (int kt = sw; kt < ntiles; kt += ATT_STREAMS) {  // workgroup-uniform
+            __syncthreads();  // every wave is done with the previous tile
 #pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            const int c = threadIdx.x + 256 * i;
-            const int key = c % ATT_KT, dc = c / ATT_KT;
-            const bool ok = (int64_t)kt * ATT_KT + key < Lk;
-            *(uint4 *)(ks + key * KP + dc * 8) = ok ? kreg[i] : make_uint4(0, 0, 0, 0);
-            const V8 vv = __builtin_bit_cast(V8, ok ? vreg[i] : make_uint4(0, 0, 0, 0));
+            for (int i = 0; i < CH; ++i) {
+                const int c = threadIdx.x + 256 * i;
+                const int key = c % ATT_KT, dc = c / ATT_KT;
+                const bool ok = (int64_t)kt * ATT_KT + key < Lk;
+                *(uint4 *)(ks + key * KP + dc * 8) = ok ? kreg[i] : make_uint4(0, 0, 0, 0);
+                const V8 vv = __builtin_bit_cast(V8, ok ? vreg[i] : make_uint4(0, 0, 0, 0));
 #pragma unroll
-            for (int e = 0; e < 8; ++e) vts[(dc * 8 + e) * ATT_VP + key] = vv[e];
+                for (int e = 0; e < 8; ++e) vts[(dc * 8 + e) * ATT_VP + key] = vv[e];
+            }
+            const int nk = next_tile(kt);  // the next tile in stream order
+            if (nk >= 0) fetch(nk);
+            __syncthreads();
+            if (active) {
+                f32x16 s;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+#pragma unroll
+                for (int kq = 0; kq < DS; ++kq) {
+                    const V8 a =
+                        __builtin_bit_cast(V8, *(const uint4 *)(ks + r * KP + 16 * kq + 8 * h2));
+                    s = AMfma<T>::mma(a, __builtin_bit_cast(V8, qf[kq]), s);
+                }
+                attn_tile<T, D>(cur, s, vts, kt, q0, qrow, off, Lk, causal, scale_log2, h2, r);
+            }
         }
-        const int nk = next_tile(kt);
-        if (nk >= 0) fetch(nk);
-        __syncthreads();
         if (active) {
-            f32x16 s;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) s[i] = 0.0f;
-#pragma unroll
-            for (int kq = 0; kq < DS; ++kq) {
-                const V8 a =
-                    __builtin_bit_cast(V8, *(const uint4 *)(ks + r * KP + 16 * kq + 8 * h2));
-                s = AMfma<T>::mma(a, __builtin_bit_cast(V8, qf[kq]), s);
-            }
-            attn_tile<T, D>(cur, s, vts, kt, q0, qrow, off, Lk, causal, scale_log2, h2, r);
-            if (nk < 0 || nk % ATT_STREAMS != kt % ATT_STREAMS) {  // stream kt % 4 ends
-                if (kt % ATT_STREAMS == 0)
-                    tot = cur;
-                else
-                    attn_merge(tot, cur.m, cur.l, [&](int t, int i) { return cur.o[t][i]; });
-                attn_init(cur);
-            }
+            if (sw == 0)
+                tot = cur;
+            else
+                attn_merge(tot, cur.m, cur.l, [&](int t, int i) { return cur.o[t][i]; });
         }
-        kt = nk;
     }
     if (!qok) return;
     T *orow = out_layout ? out + ((b * Lq + qrow) * H + hq) * D
