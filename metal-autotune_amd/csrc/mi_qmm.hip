@@ -931,13 +931,9 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
                                 *(const uint4 *)(cur + (32 * c + r) * 128 + ((chunk ^ swz) << 4));
                         }
                 // Group g = (u * S + s) * A + a is one 32-row x 16-k MFMA operand
-                // and its C MFMAs. 4-bit: group 0 is dequantized here, under the
-                // latency of the x reads, and every later group in slices between
-                // the MFMAs of the group before it (below). 8-bit keeps one
-                // dequant per group ahead of its MFMAs: its dequant is lighter,
-                // and the pipeline's extra live registers made the 128-token dual
-                // tile spill (M = 2048: 335 -> 395 us).
-                constexpr bool PIPED = BITS == 4;
+                // and its C MFMAs. Group 0 is dequantized here, under the latency
+                // of the x reads, and every later group in slices between the
+                // MFMAs of the group before it (below), at both widths.
                 typedef Dequant8<T, BITS> Dq;
                 auto dq_init = [&](Dq &d, int g) {
                     const int u = g / (S * A), s = (g / A) % S, a = g % A;
@@ -947,7 +943,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
                            (float)__builtin_bit_cast(T, (uint16_t)bq[a][u]));
                 };
                 uint32_t opa[4];  // the next MFMA operand: four packed pairs
-                if constexpr (PIPED) {
+                {
                     Dq d;
                     dq_init(d, 0);
 #pragma unroll
@@ -977,18 +973,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
                 for (int g = 0; g < NG; ++g) {
                     const int u = g / (S * A), s = (g / A) % S, a = g % A;
                     Dq d;
-                    if constexpr (!PIPED) {
-                        dq_init(d, g);
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) opa[k] = d.pair(k);
-                    }
                     const V8 af = __builtin_bit_cast(V8, (uint4){opa[0], opa[1], opa[2], opa[3]});
-                    if constexpr (!PIPED) {
-#pragma unroll
-                        for (int c = 0; c < C; ++c)
-                            acc[a][c] = Mfma<T>::mma(af, __builtin_bit_cast(V8, xf[c][u][s]), acc[a][c]);
-                        continue;
-                    }
 #pragma unroll
                     for (int c = 0; c < C; ++c) {
                         acc[a][c] = Mfma<T>::mma(af, __builtin_bit_cast(V8, xf[c][u][s]), acc[a][c]);
