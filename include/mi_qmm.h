@@ -234,9 +234,11 @@ int mi_linear_f32(const float *x, const float *w, const float *bias, float *y, i
  * order, so results are deterministic (a reassociation of the two-linear
  * stream, within fp32 rounding of it).
  * workspace: device memory of at least mi_gelu_mlp_f32_workspace_bytes(M, K, H, N)
- * bytes, 256-byte aligned, whose first bytes (the per-row-block counters) are
- * zero before its first use; every call leaves them zero again. Calls that
- * share a workspace must not overlap. */
+ * bytes, 256-byte aligned, whose first 262,144 bytes (the per-row-block
+ * counters, a fixed prefix whatever M is) are zero before its first use; every
+ * call leaves them zero again, so one workspace serves calls of any M in turn.
+ * M <= 524,280 (65,535 row blocks). Calls that share a workspace must not
+ * overlap. */
 int64_t mi_gelu_mlp_f32_workspace_bytes(int64_t M, int64_t K, int64_t H, int64_t N);
 int mi_gelu_mlp_f32(const float *x, const float *w1, const float *b1, const float *w2,
                     const float *b2, float *y, int64_t M, int64_t K, int64_t H, int64_t N,

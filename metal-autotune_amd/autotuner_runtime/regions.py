@@ -205,14 +205,17 @@ def tiny_mlp(kernel_id="tiny_mlp") -> KernelSpec:
     out0 = gelu(x W1^T + b1) W2^T + b2 with inputs (x, W1, b1, W2, b2)
     (examples/tiny_mlp.py:5-6). The hidden dimension is summed in chunks
     across workgroups in a fixed order, so the region reassociates the
-    two-linear stream (``reassociates``) and is checked at fp32 tolerance."""
+    two-linear stream (``reassociates``) and is checked at fp32 tolerance.
+    The entry covers at most 65,535 blocks of 8 rows (M <= 524,280); larger M,
+    like the other uncovered shapes, falls back to the original ops."""
     return KernelSpec(
         kernel_id=kernel_id, name="mi_gelu_mlp_f32", input_names=tuple(f"in{i}" for i in range(5)),
         output_names=("out0",), source="mi_gelu_mlp_f32",
         output_shapes=(("in0.shape[0]", "in3.shape[0]"),), output_dtypes=("float32",),
         fallback_predicate=("in0.ndim != 2 or in1.shape[1] != in0.shape[1] or "
                             "in3.shape[1] != in1.shape[0] or in0.shape[1] > 1024 or "
-                            "in0.shape[1] % 4 != 0 or in1.shape[0] % 4 != 0"),
+                            "in0.shape[1] % 4 != 0 or in1.shape[0] % 4 != 0 or "
+                            "in0.shape[0] > 524280"),
         reassociates=True)
 
 

@@ -552,12 +552,18 @@ extern "C" int mi_linear_f32(const float *x, const float *w, const float *bias, 
 
 // Workspace of mi_gelu_mlp_f32: one ticket counter per row block, then the
 // partial y tiles of every hidden chunk, 256-byte aligned.
-static int64_t mlp_tickets_bytes(int64_t M) { return ceil_div(ceil_div(M, MLP_RT) * 4, 256) * 256; }
+// The per-row-block ticket counters take a fixed prefix sized for the largest
+// grid (65535 row blocks), whatever M is: a workspace reused across calls of
+// different M then never has one call's partial sums over another call's
+// counters (a prefix sized by M let a smaller call's partials land where a
+// larger call reads its counters).
+constexpr int64_t MLP_MAX_ROW_BLOCKS = 65535;
+static int64_t mlp_tickets_bytes() { return ceil_div(MLP_MAX_ROW_BLOCKS * 4, 256) * 256; }
 
 extern "C" int64_t mi_gelu_mlp_f32_workspace_bytes(int64_t M, int64_t K, int64_t H, int64_t N) {
     (void)K;
     if (M <= 0 || H <= 0 || N <= 0) return 0;
-    return mlp_tickets_bytes(M) + ceil_div(H, MLP_HT) * M * N * (int64_t)sizeof(float);
+    return mlp_tickets_bytes() + ceil_div(H, MLP_HT) * M * N * (int64_t)sizeof(float);
 }
 
 extern "C" int mi_gelu_mlp_f32(const float *x, const float *w1, const float *b1, const float *w2,
@@ -574,13 +580,13 @@ extern "C" int mi_gelu_mlp_f32(const float *x, const float *w1, const float *b1,
     if (!x || !w1 || !w2 || !y || !workspace) return fail(MI_ERR_ARG, "null pointer");
     if (!aligned(x, 16) || !aligned(w1, 16) || !aligned(w2, 16) || !aligned(workspace, 256))
         return fail(MI_ERR_ARG, "gelu mlp: x, w1, w2 16-byte aligned, workspace 256-byte aligned");
-    if (ceil_div(M, MLP_RT) > 65535) return fail(MI_ERR_ARG, "gelu mlp: too many rows");
+    if (ceil_div(M, MLP_RT) > MLP_MAX_ROW_BLOCKS) return fail(MI_ERR_ARG, "gelu mlp: too many rows");
     const int64_t need = mi_gelu_mlp_f32_workspace_bytes(M, K, H, N);
     if (workspace_bytes < need)
         return fail(MI_ERR_ARG, "gelu mlp workspace of %lld bytes, %lld needed",
                     (long long)workspace_bytes, (long long)need);
     unsigned *tickets = (unsigned *)workspace;
-    float *part = (float *)((char *)workspace + mlp_tickets_bytes(M));
+    float *part = (float *)((char *)workspace + mlp_tickets_bytes());
     const dim3 grid((unsigned)ceil_div(H, MLP_HT), (unsigned)ceil_div(M, MLP_RT));
     const size_t lds = (size_t)(MLP_RT * K + MLP_RT * MLP_HT) * sizeof(float);
     gelu_mlp_f32_kernel<<<grid, MLP_THREADS, lds, as_stream(stream)>>>(x, w1, b1, w2, b2, y, part,

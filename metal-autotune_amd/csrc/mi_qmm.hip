@@ -1713,6 +1713,21 @@ int64_t qmm_parts_bytes(int64_t M, int64_t N, int64_t K, int gs, int bits, int d
         return 0;
     const int pitch = sbt_layout(kslice_of(K, ks, 4), gs).pitch;
     if (8ll * pitch * pitch >= (1ll << 20)) return 0;  // (the one-launch path takes it)
+    // the narrowest tile launch_parts falls back to (one 32-feature tile a
+    // wave at its token width) must fit the LDS, else the one-launch path
+    // runs the shape (its dispatcher steps down tiles, then to the GEMV)
+    QParams q = {};
+    q.K = K;
+    q.gs = gs;
+    q.ks = ks;
+    q.part = (float *)16;  // K parts as workgroups: no running sums in LDS
+    const int64_t lds = M > 64 ? (bits == 4 ? mfma_lds_bytes<bf16, 4, 1, 4>(q, 4)
+                                            : mfma_lds_bytes<bf16, 8, 1, 4>(q, 4))
+                      : M > 32 ? (bits == 4 ? mfma_lds_bytes<bf16, 4, 1, 2>(q, 4)
+                                            : mfma_lds_bytes<bf16, 8, 1, 2>(q, 4))
+                               : (bits == 4 ? mfma_lds_bytes<bf16, 4, 1, 1>(q, 4)
+                                            : mfma_lds_bytes<bf16, 8, 1, 1>(q, 4));
+    if (lds > LDS_PER_CU) return 0;
     return (int64_t)ks * M * N * (int64_t)sizeof(float);
 }
 

@@ -85,6 +85,12 @@ def test_qmm_workspace_query_needs_no_device(lib):
     assert lib.mi_qmm_workspace_bytes(128, 2560, 4096, 64, 4, 0) == 0
     assert lib.mi_qmm_workspace_bytes(8, 2560, 4096, 64, 4, 2) == 0
     assert lib.mi_qmm_workspace_bytes(128, 9728, 2560, 64, 4, 2) == 0
+    # 4-bit g32, 64 < M <= 128: the parts tile's scale/bias tables outgrow the
+    # LDS between K ~ 93k and ~184k, so the workspace entries take the
+    # one-launch path there (no workspace asked for)
+    assert lib.mi_qmm_workspace_bytes(100, 64, 92160, 32, 4, 2) == 4 * 100 * 64 * 4
+    assert lib.mi_qmm_workspace_bytes(100, 64, 96000, 32, 4, 2) == 0
+    assert lib.mi_qmm_workspace_bytes(100, 64, 160000, 32, 4, 2) == 0
 
 
 def test_argument_errors_need_no_device(lib):

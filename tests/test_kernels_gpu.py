@@ -733,8 +733,11 @@ def test_tiny_mlp_region_one_launch(M, K, H, N, biases):
 def test_tiny_mlp_calls_of_different_sizes_share_the_workspace():
     """Back-to-back calls of different row counts on one stream (one cached
     workspace): each equals the oracle, so no ticket or partial leaks from one
-    call into the next."""
-    for i, (M, H) in enumerate(((32, 1024), (9, 256), (32, 1024), (1, 64))):
+    call into the next. The sizes 1000, 300, 600 in turn are the case where a
+    ticket region sized by M let a smaller call's partial sums overwrite the
+    counters a larger call reads (the prefix is now fixed)."""
+    for i, (M, H) in enumerate(((32, 1024), (9, 256), (32, 1024), (1, 64),
+                                (1000, 256), (300, 256), (600, 256))):
         host = _mlp_inputs(1450 + i, M, 256, H, 256)
         got = ops.gelu_mlp_f32(*[to_torch(a, "float32") for a in host])
         _close(got, oracle.tiny_mlp(*[a.astype(np.float64) for a in host]), "float32", 1e-5)
