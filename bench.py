@@ -22,7 +22,22 @@ Also measured live, with HIP events on the stream the kernels run on:
     prefill and tok/s, one HIP-graph replay each);
   - cpu_baseline: the CPU oracle (the port; MLX is not installed) on a bounded
     sample -- one decoder layer at L=128 plus the lm_head for one token --
-    scaled to the 36-layer model.
+    scaled to the 36-layer model;
+  - peaks: the device's own peaks, microbenchmarked in the same run (dense
+    bf16 MFMA rate with the shader clock it held, HBM read and copy rate,
+    the per-launch floor inside a HIP graph), and every fraction reported
+    against them as well as against the spec sheet;
+  - step_clock and every kernel figure: the median of 9 samples of >= 20 ms
+    each, with min/max and the standard error of the median (the reference's
+    clock, autotuner/measure/clocks.py:30,217-231);
+  - regions_vs_ops: the region-installed model against the same model
+    running its unfused op stream (each op one library call), as the
+    reference's patched/original model ratio: ABBA/BAAB pairs, median ratio,
+    SE and agreement (clocks.py:234-287, autotuner_runtime/stats.py).
+
+The headline `value` / `ms_per_step` is the mean over exactly --steps graph
+replays bracketed by synchronizations, as the driver's contract asks;
+step_clock is the same graph sampled the reference's way.
 """
 
 from __future__ import annotations
@@ -80,19 +95,30 @@ def time_graph(g, reps, torch):
     return e0.elapsed_time(e1) / reps  # ms
 
 
-def kernel_us(make_call, n_calls, torch, reps=5):
-    """Average duration of one call: n_calls launches captured in a graph, timed
-    with events on the capture stream's successor (the current stream)."""
+def kernel_clock(make_call, n_calls, torch):
+    """Duration of one call: n_calls launches captured in a graph; the median of
+    9 samples of >= 20 ms of replays (HIP events on the current stream, which
+    follows the capture stream), in us, with its spread."""
+    import measure
+
     def body():
         for i in range(n_calls):
             make_call(i)
     g, _ = graph_of(body, torch)
     g.replay()
     torch.cuda.synchronize()
-    return time_graph(g, reps, torch) * 1000.0 / n_calls
+    c = measure.clock(g.replay, per_call=n_calls)
+    return {k: (v * 1000.0 if k in ("median", "min", "max", "se") else v) for k, v in c.items()}
 
 
-def qmm_config2(torch, ops):
+def spread_us(c):
+    """The spread fields of a kernel_clock result, rounded."""
+    return {"median_us": round(c["median"], 3), "min_us": round(c["min"], 3),
+            "max_us": round(c["max"], 3), "se_us": round(c["se"], 4), "samples": c["n"],
+            "calls_per_sample": c["calls_per_sample"]}
+
+
+def qmm_config2(torch, ops, peaks=None):
     """Config 2: x[M, 2560] bf16 @ W[9728, 2560]^T, 4-bit g64, M in {1, 128}."""
     from workloads.quantize import random_quantized
 
@@ -107,20 +133,26 @@ def qmm_config2(torch, ops):
         x = torch.randn((M, K), generator=gen, device="cuda").to(torch.bfloat16)
         y = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
         from autotuner_runtime import hip
-        us = kernel_us(lambda i: hip.b_qmm([x, *ws[i % copies]], [y], {"group_size": gs, "bits": 4}),
-                       4 * copies, torch)
+        c = kernel_clock(lambda i: hip.b_qmm([x, *ws[i % copies]], [y], {"group_size": gs, "bits": 4}),
+                         4 * copies, torch)
+        us = c["median"]
         byts = wbytes + 2 * M * K + 2 * M * N
         fl = 2 * M * N * K
         out[f"M{M}"] = {"us": round(us, 2), "GB_s": round(byts / us / 1e3, 1),
                         "hbm_frac": round(byts / us / 1e3 / HBM_PEAK_GBS, 4),
                         "TFLOP_s": round(fl / us / 1e6, 2),
                         "mfma_frac": round(fl / us / 1e6 / BF16_PEAK_TFS, 4),
-                        "bytes": byts, "flops": fl}
+                        "bytes": byts, "flops": fl, "clock": spread_us(c)}
+        if peaks:
+            out[f"M{M}"]["hbm_frac_measured_peak"] = round(
+                byts / us / 1e3 / peaks["hbm"]["read_GB_s"], 4)
+            out[f"M{M}"]["mfma_frac_measured_peak"] = round(
+                fl / us / 1e6 / peaks["mfma_bf16"]["TF_s"], 4)
     del ws
     return out
 
 
-def dominant_kernel(model, torch, ops):
+def dominant_kernel(model, torch, ops, peaks=None):
     """The gate/up region (dual qmm + swiglu epilogue) at M=128 over the 36
     layers' weights: 2 x 128 x 9728 x 2560 x 2 flops per launch."""
     layers = [l.wrapped if hasattr(l, "wrapped") else l for l in model.model.layers]
@@ -131,7 +163,8 @@ def dominant_kernel(model, torch, ops):
         g, u = m.gate_proj, m.up_proj
         ops.qmm_dual(x, g.weight, g.scales, g.biases, u.weight, u.scales, u.biases, swiglu=True)
 
-    us = kernel_us(call, 2 * len(layers), torch)
+    c = kernel_clock(call, 2 * len(layers), torch)
+    us = c["median"]
     N, K = model.cfg.intermediate_size, model.cfg.hidden_size
     fl = 2 * 2 * PROMPT * N * K
     tf = fl / us / 1e6
@@ -142,11 +175,50 @@ def dominant_kernel(model, torch, ops):
     if tf_file.exists():
         found = re.search(r"^hbm_bytes_per_launch = (\d+)$", tf_file.read_text(), re.M)
         traffic = int(found.group(1)) if found else None
-    return {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFS, "unit": "TFLOP/s",
-            "frac": round(tf / BF16_PEAK_TFS, 4), "traffic": traffic,
-            "kernel": "qmm_mfma_mixed3_kernel (dual gate/up + swiglu epilogue, 128/64/32-token tiles)",
-            "shape": f"M={PROMPT} N=2x{N} K={K} 4-bit g64", "avg_us": round(us, 2),
-            "flops_per_launch": fl}
+    out = {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFS, "unit": "TFLOP/s",
+           "frac": round(tf / BF16_PEAK_TFS, 4), "traffic": traffic,
+           "kernel": "qmm_mfma_mixed3_kernel (dual gate/up + swiglu epilogue, 128/64/32-token tiles)",
+           "shape": f"M={PROMPT} N=2x{N} K={K} 4-bit g64", "avg_us": round(us, 2),
+           "flops_per_launch": fl, "clock": spread_us(c)}
+    if peaks:
+        out["peak_measured"] = peaks["mfma_bf16"]["TF_s"]
+        out["frac_measured_peak"] = round(tf / peaks["mfma_bf16"]["TF_s"], 4)
+    return out
+
+
+def regions_vs_ops(torch, ops, qwen3, ids) -> dict:
+    """The region-installed model (candidate) against the same seeded model
+    running its op stream (baseline): one graph replay per prefill each, paired
+    ABBA/BAAB samples of >= 20 ms. Ratio < 1: the regions are faster."""
+    import measure
+
+    cfg = qwen3.Qwen3Config()
+    graphs = {}
+    for arm in ("ops", "regions"):
+        model = qwen3.build(cfg, seed=0)
+        if arm == "regions":
+            qwen3.install_regions(model)
+        caches = model.make_cache(PROMPT)
+
+        def step(model=model, caches=caches):
+            for c in caches:
+                c.offset = 0
+            return ops.argmax(model(ids, caches).reshape(1, -1))
+
+        g, tok = graph_of(step, torch)
+        graphs[arm] = (g, model, caches, tok)
+    r = measure.compare(graphs["ops"][0].replay, graphs["regions"][0].replay)
+    same = int(graphs["ops"][3].item()) == int(graphs["regions"][3].item())
+    del graphs
+    torch.cuda.empty_cache()
+    return {"model_ratio": round(r["median_ratio"], 4),
+            "ops_ms": round(r["median_base_ms"], 4), "regions_ms": round(r["median_cand_ms"], 4),
+            "median_delta_ms": round(r["median_delta_ms"], 4),
+            "se_delta_ms": round(r["se_delta_ms"], 4), "stability": round(r["stability"], 3),
+            "observations": r["observations"], "replays_per_sample": r["calls_per_sample"],
+            "greedy_tokens_equal": same,
+            "baseline": "the same seeded model, regions not installed: its op stream (each op "
+                        "one call of this library), not MLX's kernels (MLX is not installed)"}
 
 
 def cpu_baseline(model, ids, torch):
@@ -207,11 +279,12 @@ def cpu_baseline(model, ids, torch):
                       "in numpy; MLX CPU backend unavailable (mlx not installed, no network)"}
 
 
-def lfm2_config5(torch, ops, reps: int = 10) -> dict:
+def lfm2_config5(torch, ops) -> dict:
     """Config 5 beside the headline: the LFM2-1.2B-shaped hybrid (16 layers:
     10 gated short-conv, 6 attention; hidden 2048, SwiGLU 8192, tied
     V = 65536) prefilling 2048 seeded token ids, 4- and 8-bit, region cuts
-    installed; one HIP-graph replay per prefill, timed with HIP events."""
+    installed; one HIP-graph replay per prefill, the median of 9 samples of
+    >= 20 ms of replays (HIP events)."""
     from workloads import lfm2, qwen3
 
     out = {"workload": "config 5: LFM2-1.2B-shaped hybrid, 16 layers, g64, tied V=65536, "
@@ -233,10 +306,14 @@ def lfm2_config5(torch, ops, reps: int = 10) -> dict:
         g, tok = graph_of(step, torch)
         g.replay()
         torch.cuda.synchronize()
-        ms = time_graph(g, reps, torch)
+        import measure
+        c = measure.clock(g.replay)
+        ms = c["median"]
         out[f"{bits}bit"] = {"ms_per_prefill": round(ms, 3),
                              "tok_s": round(2048 / (ms / 1000.0), 1),
-                             "greedy_token": int(tok.item())}
+                             "greedy_token": int(tok.item()),
+                             "min_ms": round(c["min"], 3), "max_ms": round(c["max"], 3),
+                             "se_ms": round(c["se"], 4), "samples": c["n"]}
         del g, model, caches
         torch.cuda.empty_cache()
     return out
@@ -280,13 +357,30 @@ def main():
     ms = e0.elapsed_time(e1) / args.steps
     token = int(tok.item())
 
-    roof = dominant_kernel(model, torch, ops)
-    qmm = qmm_config2(torch, ops)
+    import measure
+    sc = measure.clock(g.replay)
+    step_clock = {"median_ms": round(sc["median"], 4), "min_ms": round(sc["min"], 4),
+                  "max_ms": round(sc["max"], 4), "se_ms": round(sc["se"], 5),
+                  "iqr_rel": round(sc["iqr_rel"], 4), "samples": sc["n"],
+                  "replays_per_sample": sc["calls_per_sample"],
+                  "tok_s_at_median": round(PROMPT / (sc["median"] / 1000.0), 1)}
+    peaks = measure.peaks()
+    peaks_line = {"mfma_bf16_TF_s": peaks["mfma_bf16"]["TF_s"],
+                  "mfma_bf16_by_occupancy": peaks["mfma_bf16"]["by_occupancy"],
+                  "shader_clock_GHz": peaks["mfma_bf16"]["shader_clock_GHz_one_wave_per_simd"],
+                  "hbm_read_GB_s": peaks["hbm"]["read_GB_s"],
+                  "hbm_copy_GB_s": peaks["hbm"]["copy_GB_s"],
+                  "graph_launch_us": peaks["graph_launch"]["us"],
+                  "spec": {"mfma_bf16_TF_s": BF16_PEAK_TFS, "hbm_GB_s": HBM_PEAK_GBS}}
+
+    roof = dominant_kernel(model, torch, ops, peaks)
+    qmm = qmm_config2(torch, ops, peaks)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(model, ids, torch)
     del g, model, caches
     torch.cuda.empty_cache()
+    rvo = regions_vs_ops(torch, ops, qwen3, ids)
     hybrid = None if args.no_lfm2 else lfm2_config5(torch, ops)
     line = {
         "metric": "prefill tok/s Qwen3-4B-shape 4-bit @128 tok; qmm HBM GB/s and MFMA % of peak",
@@ -307,6 +401,9 @@ def main():
                    "global_batch": 1, "seq_len": PROMPT, "parallelism": "single GPU",
                    "greedy_token": token},
         "roofline": roof,
+        "step_clock": step_clock,
+        "peaks": peaks_line,
+        "regions_vs_ops": rvo,
         "qmm": qmm,
         "lfm2_config5": hybrid,
         "cpu_baseline": cpu,

@@ -274,7 +274,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QParams p) {
         float sc[P], bi[P];
 #pragma unroll
         for (int q = 0; q < P; ++q) {
-            const uint4 wv = ld16(wr[q] + c * 4);
+            const uint4 wv = ld16_nt(wr[q] + c * 4);
             const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
             for (int i = 0; i < VPC; ++i)
@@ -412,7 +412,7 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
             const int64_t g = (cc * 32) >> p.gs_log2;
 #pragma unroll
             for (int q = 0; q < P; ++q) {
-                wv[q][i] = ld16(wr[q] + 4 * cc);
+                wv[q][i] = ld16_nt(wr[q] + 4 * cc);
                 sv[q][i] = sr[q][g];
                 bv[q][i] = br[q][g];
             }

@@ -530,3 +530,39 @@ def lfm2_attn_layer(x, W: dict, cfg, offset: int, kcache, vcache, dtype: str = "
     h = round_to(np.asarray(x, np.float64) + _qmm_auto(o, W["out_proj"], gs, bits, dtype), dtype)
     hn = rms_norm(h, W["ffn_norm"], eps, dtype)
     return lfm2_mlp(hn, h, W, cfg, dtype)
+
+
+def lfm2_layer_window(x, W: dict, cfg, kind: str, rows: int, dtype: str = "bfloat16"):
+    """Output rows [L - rows, L) of one LFM2 layer over its whole input x
+    [1, L, hidden] (fresh state, offset 0), computed on only what those rows
+    read. A conv layer's row t reads input rows t-2..t (the 3-tap causal conv
+    over B*x, wrappers.py:57-66; everything else is row-wise), so the window
+    runs on rows + 2 input rows from a zero state and drops the two context
+    rows. An attention layer's window attends to every earlier row: the keys
+    and values of rows [0, L - rows) are the cache update of
+    lfm2_attn_layer on those rows (row-wise: rms_norm, k/v qmm, k-norm + RoPE
+    at offset 0), and the window runs as the next chunk at offset L - rows
+    (mlx-lm's chunked prefill). The same values as lfm2_attn_layer /
+    lfm2_conv_layer over the whole x, restricted to the window, bit for bit,
+    when every projection sees more than 8 rows in both forms: _qmm_auto
+    routes M <= 8 to the factored qmv (stitch.py:74-100), so a shorter window
+    or key prefix would round its projections differently."""
+    L = x.shape[1]
+    s = L - rows
+    if rows < 9 or rows > L or (kind != "conv" and 0 < s < 9):
+        raise ValueError(f"window of {rows} rows over {L}: the window, and an attention "
+                         "layer's key prefix, need more than 8 rows")
+    if kind == "conv":
+        y, _ = lfm2_conv_layer(x[:, max(s - 2, 0):], W, cfg, None, dtype)
+        return y[:, min(s, 2):]
+    gs, bits, eps = cfg.group_size, cfg.bits, cfg.norm_eps
+    HK, D = cfg.num_key_value_heads, cfg.head_dim
+    kc = np.zeros((1, HK, L, D), np.float32)
+    vc = np.zeros_like(kc)
+    if s > 0:
+        xn = rms_norm(x[:, :s], W["operator_norm"], eps, dtype)
+        kc[:, :, :s] = norm_rope(_qmm_auto(xn, W["k_proj"], gs, bits, dtype), W["k_layernorm"],
+                                 eps, HK, D, cfg.rope_theta, 0, dtype)
+        vc[:, :, :s] = norm_rope(_qmm_auto(xn, W["v_proj"], gs, bits, dtype), None, 0.0, HK, 0,
+                                 1.0, 0, dtype)
+    return lfm2_attn_layer(x[:, s:], W, cfg, s, kc, vc, dtype)

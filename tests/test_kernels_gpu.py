@@ -138,9 +138,16 @@ def test_qmm_dtypes_bits_groups(dtype, bits, gs, M):
     x = oracle.round_to(r.normal(0, 1, (M, K)), dtype)
     wq, s, b = _quant(9 + bits, N, K, gs, bits, dtype)
     y = ops.quantized_matmul(to_torch(x, dtype), *_dev(wq, s, b, dtype), group_size=gs, bits=bits)
-    want = oracle.quantized_matmul(x, wq, s, b, gs, bits, dtype)
-    tol = 2e-5 if dtype == "float32" else None
-    _close(y, want, dtype, tol)
+    if dtype == "float32":
+        # fp32 runs the per-group factored sum at every M (the GEMV kernels;
+        # the MFMA tiles take 16-bit T only): held to north_star's fp32 bar
+        # against the oracle's restatement of that same algorithm
+        # (scaffold/lower.py:1179-1233), and to twice it against the
+        # dequantize-first form
+        _close(y, oracle.qmm_factored(x, wq, s, b, gs, bits, dtype), dtype, 1e-5)
+        _close(y, oracle.quantized_matmul(x, wq, s, b, gs, bits, dtype), dtype, 2e-5)
+    else:
+        _close(y, oracle.quantized_matmul(x, wq, s, b, gs, bits, dtype), dtype)
 
 
 @pytest.mark.parametrize("M", [1, 64, 128])

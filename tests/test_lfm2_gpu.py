@@ -140,30 +140,52 @@ def _hidden_states(model, ids, caches):
     return hs, logits
 
 
+WINDOW = 128  # teacher-forced rows per layer: the last WINDOW positions of the prompt
+
+
+def _teacher_forced_window(layer, x_in, cfg):
+    """The oracle's output over the last WINDOW rows of one layer given the
+    GPU's own whole input to it (oracle.lfm2_layer_window)."""
+    base = layer.wrapped if hasattr(layer, "wrapped") else layer
+    kind = "conv" if hasattr(base, "conv") else "attn"
+    return oracle.lfm2_layer_window(x_in, export_layer(layer), cfg, kind, WINDOW)
+
+
 @pytest.mark.gpu
-@pytest.mark.timeout(600)
+@pytest.mark.timeout(900)
 @pytest.mark.parametrize("bits", [4, 8])
 def test_lfm2_model_config5_prefill(bits):
     """Config 5: 16 layers (conv at 0,1,3,4,6,7,9,11,13,15; attention at
-    2,5,8,10,12,14), 4- and 8-bit, tied V=65536, a 2048-token prefill.
+    2,5,8,10,12,14), 4- and 8-bit, tied V=65536, a 2048-token prefill, then one
+    greedy decode step through the carried KV caches and conv states.
 
     (a) the region-installed model equals the original op streams bit for
         bit, layer by layer and at the logits;
-    (b) teacher-forced: the oracle's conv layer 0 and attention layer 2 on
-        the GPU's own layer inputs, <= 1e-2;
+    (b) teacher-forced, every one of the 16 layers: the oracle layer on the
+        GPU's own input to it, <= 1e-2 over the last 128 positions (conv
+        layer 0 and attention layer 2 also over all 2048);
     (c) the final norm + tied lm_head on the GPU's last hidden state <= 1e-2,
-        and the greedy token equal to the oracle's.
+        and the greedy token equal to the oracle's;
+    (d) the decode step: every layer teacher-forced against the oracle layer
+        on the GPU's decode input and the GPU's prefill state (its KV cache or
+        conv state), <= 1e-2; the final norm + lm_head on the GPU's decode
+        hidden state <= 1e-2 with the same greedy token; and the oracle's own
+        chain of all 16 layers from the decoded token's embedding, over those
+        states, gives the same token wherever its top-2 margin exceeds twice
+        its drift from the GPU's logits.
     """
     from autotuner_runtime import ops
     from workloads import lfm2, qwen3
 
     cfg = lfm2.Lfm2Config(bits=bits)
     model = lfm2.build(cfg, seed=0)
-    ids = qwen3.tokens(11, 2048, cfg.vocab_size)
-    hs_o, lg_o = _hidden_states(model, ids, model.make_cache(2048))
+    L = 2048
+    ids = qwen3.tokens(11, L, cfg.vocab_size)
+    hs_o, lg_o = _hidden_states(model, ids, model.make_cache(L + 1))
     hs_o = [to_np(h) for h in hs_o]
     lfm2.install_regions(model)
-    hs_r, lg_r = _hidden_states(model, ids, model.make_cache(2048))
+    caches = model.make_cache(L + 1)
+    hs_r, lg_r = _hidden_states(model, ids, caches)
     torch.cuda.synchronize()
     for i, h in enumerate(hs_r):
         assert np.array_equal(to_np(h), hs_o[i]), f"layer {i}: regions changed the bits"
@@ -171,11 +193,16 @@ def test_lfm2_model_config5_prefill(bits):
     hs = [to_np(h) for h in hs_r]
 
     inner = model.model
-    W0, W2 = export_layer(inner.layers[0]), export_layer(inner.layers[2])
+    layers = list(inner.layers)
+    W0, W2 = export_layer(layers[0]), export_layer(layers[2])
     want0, _ = oracle.lfm2_conv_layer(hs[0], W0, cfg, None)
     e0 = _close(hs[1], want0)
-    kc = np.zeros((1, cfg.num_key_value_heads, 2048, cfg.head_dim), np.float32)
+    kc = np.zeros((1, cfg.num_key_value_heads, L, cfg.head_dim), np.float32)
     e2 = _close(hs[3], oracle.lfm2_attn_layer(hs[2], W2, cfg, 0, kc, np.zeros_like(kc)))
+    errs = []
+    for i, layer in enumerate(layers):
+        want = _teacher_forced_window(layer, hs[i], cfg)
+        errs.append(_close(hs[i + 1][:, L - WINDOW:], want))
 
     emb = _lin(inner.embed_tokens)
     hn = oracle.rms_norm(hs[-1][:, -1:], to_np(inner.embedding_norm.weight), cfg.norm_eps,
@@ -186,10 +213,64 @@ def test_lfm2_model_config5_prefill(bits):
     tok = int(ops.argmax(lg_r.reshape(1, -1)).item())
     top2 = np.sort(want)[-2:]
     margin, abs_err = float(top2[1] - top2[0]), float(np.abs(got - want).max())
-    print(f"\nconfig5 {bits}-bit prefill 2048: conv layer 0 {e0:.3e}, attention layer 2 "
-          f"{e2:.3e}, logits {el:.3e} (top-2 margin {margin:.3e}, max abs err {abs_err:.3e}), "
-          f"greedy token gpu {tok} oracle {int(np.argmax(want))}")
+    print(f"\nconfig5 {bits}-bit prefill {L}: conv layer 0 {e0:.3e}, attention layer 2 "
+          f"{e2:.3e} (whole prompt); every layer over the last {WINDOW} rows "
+          f"max {max(errs):.3e}; logits {el:.3e} (top-2 margin {margin:.3e}, max abs err "
+          f"{abs_err:.3e}), greedy token gpu {tok} oracle {int(np.argmax(want))}")
     assert tok == int(np.argmax(want)), "greedy token differs from the oracle's"
+
+    # (d) one decode step through the carried states
+    states = []
+    for layer, c in zip(layers, caches):
+        base = layer.wrapped if hasattr(layer, "wrapped") else layer
+        if hasattr(base, "conv"):
+            states.append(to_np(c.state).copy())
+        else:
+            states.append((to_np(c.keys).copy(), to_np(c.values).copy()))
+    nxt = torch.tensor([[tok]], dtype=torch.int64, device="cuda")
+    hd, lg_d = _hidden_states(model, nxt, caches)
+    torch.cuda.synchronize()
+    hd = [to_np(h) for h in hd]
+    assert all(c.offset == L + 1 for c in caches)
+
+    def oracle_layer(i, x):
+        W = export_layer(layers[i])
+        st = states[i]
+        if isinstance(st, tuple):
+            kc, vc = st[0].copy(), st[1].copy()
+            return oracle.lfm2_attn_layer(x, W, cfg, L, kc, vc)
+        return oracle.lfm2_conv_layer(x, W, cfg, st)[0]
+
+    derrs = [_close(hd[i + 1], oracle_layer(i, hd[i])) for i in range(len(layers))]
+    # the final norm + tied lm_head on the GPU's decode hidden state
+    norm_w = to_np(inner.embedding_norm.weight)
+
+    def head(x):
+        hn = oracle.rms_norm(x, norm_w, cfg.norm_eps, "bfloat16")
+        return oracle.qmm_factored(hn, *emb, cfg.group_size, cfg.bits, "bfloat16").reshape(-1)
+
+    got_d = to_np(lg_d).reshape(-1)
+    want_d = head(hd[-1])
+    ed = _close(got_d, want_d)
+    tok_d = int(ops.argmax(lg_d.reshape(1, -1)).item())
+    assert tok_d == int(np.argmax(want_d)), "decode greedy token differs from the oracle's"
+    # the oracle's own 16-layer chain from the embedding of the decoded token
+    # (not teacher-forced: bf16 roundings drift apart layer by layer, so its
+    # logits are reported, and its token must agree wherever its top-2 margin
+    # exceeds the drift)
+    xo = oracle.dequantize(*emb, cfg.group_size, cfg.bits, "bfloat16")[[tok]][None]
+    assert np.array_equal(hd[0], xo)
+    for i in range(len(layers)):
+        xo = oracle_layer(i, xo)
+    chain = head(xo)
+    drift = float(np.abs(got_d - chain).max())
+    top2 = np.sort(chain)[-2:]
+    print(f"config5 {bits}-bit decode at {L}: layers teacher-forced max {max(derrs):.3e}, logits "
+          f"{ed:.3e}, greedy token gpu {tok_d} oracle {int(np.argmax(want_d))}; oracle chain: "
+          f"token {int(np.argmax(chain))}, logits drift {drift:.3e}, top-2 margin "
+          f"{float(top2[1] - top2[0]):.3e}")
+    if float(top2[1] - top2[0]) > 2 * drift:
+        assert tok_d == int(np.argmax(chain)), "decode token differs from the oracle chain's"
 
 
 @pytest.mark.gpu

@@ -564,3 +564,33 @@ def test_layer_with_factored_projections_stays_within_the_bar():
     a = oracle.qwen3_layer(x, W, cfg, 0, kc.copy(), kc.copy(), qmm=proj)
     b = oracle.qwen3_layer(x, W, cfg, 0, kc.copy(), kc.copy())
     assert np.abs(a - b).max() <= 1e-2 * np.abs(b).max()
+
+
+@pytest.mark.parametrize("kind", ["conv", "attn"])
+@pytest.mark.parametrize("rows", [9, 16, 31])
+def test_lfm2_layer_window_equals_the_whole_layer(kind, rows):
+    """oracle.lfm2_layer_window (the teacher-forced window of the config-5 GPU
+    test) gives the whole layer's last rows bit for bit: the conv window's two
+    context rows and the attention window's key/value prefix carry exactly
+    what those rows read (a window without the context rows, or without the
+    prefix, fails)."""
+    cfg, W = _tiny_lfm2(60)
+    L = 40
+    x = oracle.round_to(rng(61).normal(0, 1, (1, L, 128)), "bfloat16")
+    if kind == "conv":
+        whole, _ = oracle.lfm2_conv_layer(x, W, cfg, None)
+    else:
+        kc, vc = _caches(cfg, L)
+        whole = oracle.lfm2_attn_layer(x, W, cfg, 0, kc, vc)
+    got = oracle.lfm2_layer_window(x, W, cfg, kind, rows)
+    assert got.shape == (1, rows, 128)
+    assert np.array_equal(got, whole[:, L - rows:])
+    # the window alone (no context rows / no key prefix) is a different answer
+    if kind == "conv":
+        alone, _ = oracle.lfm2_conv_layer(x[:, L - rows:], W, cfg, None)
+    else:
+        kc, vc = _caches(cfg, L)
+        alone = oracle.lfm2_attn_layer(x[:, L - rows:], W, cfg, 0, kc, vc)
+    assert not np.array_equal(alone, whole[:, L - rows:])
+    with pytest.raises(ValueError):  # projections of <= 8 rows route to the qmv form
+        oracle.lfm2_layer_window(x, W, cfg, kind, 8)
