@@ -78,8 +78,10 @@ def graph_of(fn, torch):
         fn()  # eager run: allocations and library loading happen outside capture
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
+    from autotuner_runtime import hip
+
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with hip.graph_workspaces(), torch.cuda.graph(g):  # scratch owned by this graph
         out = fn()
     torch.cuda.synchronize()
     return g, out

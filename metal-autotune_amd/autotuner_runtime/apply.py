@@ -1,11 +1,13 @@
 """apply(): install an artifact's regions onto a freshly built model.
 
-The reference's apply.py:19-60 on torch modules: read ``swap_table.json``
-(entries of scope_path, wrapper_class, kernel_ids), load the wrapper classes
-from ``patch/wrappers.py`` and the region specs from
-``kernels/<id>.launch.json`` (+ ``<id>.hip`` naming the entry point), and swap
-a wrapper instance in at each scope address. A root-scope entry ("") returns
-the wrapper in place of the model, so callers use the return value.
+The same contract as the reference's apply (autotuner_runtime/apply.py:19-60),
+on torch modules: the artifact's swap table lists, per scope address, the
+wrapper class (from the generated ``patch/wrappers.py``) and the region kernel
+ids it runs (``kernels/<id>.launch.json`` + ``<id>.hip`` naming the entry
+point). Each listed scope gets a wrapper around what it holds now; a wrapper
+at the root address ("") stands in for the model itself, so callers keep the
+return value. ``baseline=True`` installs the artifact's baseline table and
+wrappers, which run no region kernels.
 """
 
 from __future__ import annotations
@@ -13,37 +15,44 @@ from __future__ import annotations
 import importlib.util
 import json
 from pathlib import Path
+from types import ModuleType
 
 from . import kernels as _kernels
 from .swap import install, resolve
 
 
 def load_specs(artifact_dir: str | Path) -> dict:
-    specs = {}
-    for launch in sorted((Path(artifact_dir) / "kernels").glob("*.launch.json")):
-        spec = _kernels.load_spec(launch)
-        specs[spec.kernel_id] = spec
-    return specs
+    """Every region spec of an artifact, by kernel id."""
+    found = (_kernels.load_spec(p)
+             for p in sorted((Path(artifact_dir) / "kernels").glob("*.launch.json")))
+    return {spec.kernel_id: spec for spec in found}
+
+
+def _wrapper_module(source: Path) -> ModuleType:
+    """The generated wrapper classes, imported from their file (no package)."""
+    loader_spec = importlib.util.spec_from_file_location("mi_patch_wrappers", source)
+    module = importlib.util.module_from_spec(loader_spec)
+    loader_spec.loader.exec_module(module)
+    return module
 
 
 def apply(model: object, artifact_dir: str | Path, *, baseline: bool = False) -> object:
-    artifact_dir = Path(artifact_dir)
-    prefix = "baseline_" if baseline else ""
-    table = json.loads((artifact_dir / f"{prefix}swap_table.json").read_text())
-    module_spec = importlib.util.spec_from_file_location(
-        "mi_patch_wrappers", artifact_dir / "patch" / f"{prefix}wrappers.py")
-    wrappers = importlib.util.module_from_spec(module_spec)
-    module_spec.loader.exec_module(wrappers)
-    specs = {} if baseline else load_specs(artifact_dir)
+    root = Path(artifact_dir)
+    stem = "baseline_" if baseline else ""
+    entries = json.loads((root / f"{stem}swap_table.json").read_text())
+    classes = _wrapper_module(root / "patch" / f"{stem}wrappers.py")
+    by_id = {} if baseline else load_specs(root)
 
-    patched = model
-    for entry in table:
-        cls = getattr(wrappers, entry["wrapper_class"])
-        kernel_specs = {kid: specs[kid] for kid in entry["kernel_ids"]}
-        path = entry["scope_path"]
-        if path == "":
-            patched = cls(patched, kernel_specs)
-        else:
-            _, _, original = resolve(patched, path)
-            install(patched, path, cls(original, kernel_specs))
-    return patched
+    def wrapper_for(entry: dict, target: object) -> object:
+        wrapper_cls = getattr(classes, entry["wrapper_class"])
+        return wrapper_cls(target, {kid: by_id[kid] for kid in entry["kernel_ids"]})
+
+    top = model
+    for entry in entries:
+        address = entry["scope_path"]
+        if not address:
+            top = wrapper_for(entry, top)  # the wrapper replaces the model
+            continue
+        current = resolve(top, address)[2]
+        install(top, address, wrapper_for(entry, current))
+    return top

@@ -38,6 +38,9 @@ kernel's host-side dispatch.
 
 Streams: capture and replay run on the caller's current stream. Graphs hold
 no ``hipMemsetAsync`` nodes: every library kernel writes its outputs in full.
+Each graph is captured inside its own ``hip.graph_workspaces()`` scope, so the
+scratch buffers its kernels address (K-part sums, MLP tickets) belong to it
+alone: two graphs replayed side by side on different streams never share one.
 """
 
 from __future__ import annotations
@@ -179,7 +182,8 @@ class GraphWrapper(nn.Module):
         start = [dict(vars(h)) for h in holders]
         static_args = [a.clone() if isinstance(a, torch.Tensor) else a for a in args]
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        from . import hip  # (the binding; imported here to keep graph.py torch-only at import)
+        with hip.graph_workspaces(), torch.cuda.graph(graph):
             outputs = self.wrapped(*static_args)
         writes = []
         for i, (h, saved) in enumerate(zip(holders, start)):

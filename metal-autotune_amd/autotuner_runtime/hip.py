@@ -13,6 +13,7 @@ shapes a kernel does not cover), and launches on torch's current stream.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -435,24 +436,52 @@ def b_linear_f32(ins, outs, p):
                                int(p.get("act", MI_ACT_NONE)), _stream(x)), "linear_f32")
 
 
-# Workspaces of mi_gelu_mlp_f32 per (device, stream): their ticket counters
-# start at zero (torch.zeros) and every call leaves them zero, so one buffer
-# serves every later call on that stream (calls on one stream never overlap).
-# Workspaces per (kind, device, stream), zero-filled when made. Calls on one
-# stream run in order, so they share it. A workspace that has to grow is
-# replaced and the old one kept alive: a HIP graph captured with it still
-# addresses it.
+# Workspaces (the K-part sums of the _ws qmm entries, mi_gelu_mlp_f32's
+# tickets and partial sums), zero-filled when made; mi_gelu_mlp_f32 leaves its
+# tickets zero after every call.
+#
+# Eager calls share one workspace per (kind, device, stream): calls on one
+# stream run in order. A call under HIP graph capture bakes the workspace's
+# address into the graph, and graphs may later replay on different streams at
+# the same time, so a captured call never takes an eager stream's workspace:
+# inside graph_workspaces() every graph captured in the scope shares the
+# scope's own workspaces (its calls are stream-ordered), and a capture outside
+# such a scope gives each call a workspace of its own. Either way the buffer is
+# kept alive as long as the process, since a graph may replay at any time; a
+# workspace that has to grow is replaced and the old one kept alive too.
 _workspaces: dict[tuple, torch.Tensor] = {}
 _retired: list[torch.Tensor] = []
+_scope = threading.local()
+
+
+@contextlib.contextmanager
+def graph_workspaces():
+    """A scope whose graph captures share workspaces of their own (no other
+    graph or stream uses them). GraphWrapper captures each graph in one."""
+    prev = getattr(_scope, "token", None)
+    _scope.token = object()
+    try:
+        yield
+    finally:
+        _scope.token = prev
 
 
 def _workspace(kind: str, device, stream: int, nbytes: int, minimum: int = 4096) -> torch.Tensor:
-    key = (kind, device, stream)
+    size = max(nbytes, minimum)
+    if torch.cuda.is_current_stream_capturing():
+        token = getattr(_scope, "token", None)
+        if token is None:  # a capture of its own: a workspace per call
+            ws = torch.zeros(size, dtype=torch.uint8, device=device)
+            _retired.append(ws)
+            return ws
+        key = (kind, device, token)
+    else:
+        key = (kind, device, stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         if ws is not None:
             _retired.append(ws)
-        ws = torch.zeros(max(nbytes, minimum), dtype=torch.uint8, device=device)
+        ws = torch.zeros(size, dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
 

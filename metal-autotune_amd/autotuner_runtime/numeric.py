@@ -7,8 +7,10 @@ Same policy as the reference's numeric.py:1-122, on torch tensors:
   first; non-float outputs (indices, packed words) must match exactly
   whatever the tolerance; then the non-finite pattern (finite where finite,
   NaN where NaN, same signed inf where inf); then elementwise
-  ``|c - r| <= max(atol + rtol*|r|, wobble_floor)``, evaluated in float64
-  (exact differences, no overflow), failing closed on a NaN error;
+  ``|c - r| <= max(atol + rtol*|r|, wobble_floor)``, evaluated in float32
+  as the reference does (numeric.py:83-96), an overflowing difference
+  re-evaluated on both sides scaled by max(|c|, |r|, 1), failing closed on
+  a NaN error;
 * ``tolerance_for(dtype)`` gives the per-dtype defaults
   (fp32 (1e-5, 1e-6), fp16 (1e-2, 2e-2), bf16 (2e-2, 4e-2)).
 
@@ -109,10 +111,12 @@ def compare(candidate: torch.Tensor, reference: torch.Tensor, rtol: float, atol:
     """Tolerance comparison: per element |c - r| <= max(atol + rtol*|r|,
     wobble_floor) after the non-finite pattern rule.
 
-    The float32 values are compared in float64, where their difference is
-    exact and cannot overflow (3e38 against -3e38 is a distance of 6e38, not
-    an infinity that a huge tolerance might absorb). Integer and boolean
-    outputs must be equal whatever the tolerance."""
+    Both sides and the allowance are float32, so a value at the boundary
+    passes or fails exactly as in the reference (numeric.py:83-96). Where the
+    float32 excess is NaN (an overflowing difference against an infinite
+    allowance) it is taken again with both sides divided by max(|c|, |r|, 1):
+    3e38 against -3e38 stays a failure instead of an accidental pass. Integer
+    and boolean outputs must be equal whatever the tolerance."""
     validate_tolerances((rtol, atol))
     bad = _same_structure(candidate, reference, float("inf"))
     if bad is not None:
@@ -127,15 +131,22 @@ def compare(candidate: torch.Tensor, reference: torch.Tensor, rtol: float, atol:
             return CompareResult(False, "tolerance", float("inf"), _first(differs),
                                  "integer/boolean outputs must be equal; tolerances do not apply")
         return CompareResult(True, "", 0.0, None)
-    c = cand.to(torch.float64)
-    r = ref.to(torch.float64)
+    c = cand.to(torch.float32)
+    r = ref.to(torch.float32)
     broken = ~nonfinite_pattern_ok(c, r)
     if bool(broken.any()):
         return CompareResult(False, "nonfinite_pattern", float("inf"), _first(broken),
                              f"{int(broken.sum())} elements break the non-finite pattern")
     finite = torch.isfinite(r)
-    budget = torch.clamp(atol + rtol * r.abs(), min=wobble_floor)
+
+    def f32(v):
+        return torch.tensor(v, dtype=torch.float32, device=r.device)
+
+    budget = torch.maximum(f32(atol) + f32(rtol) * r.abs(), f32(wobble_floor))
     excess = torch.where(finite, (c - r).abs() - budget, torch.zeros_like(r))
+    scale = torch.clamp(torch.maximum(c.abs(), r.abs()), min=1.0)
+    scaled = (c / scale - r / scale).abs() - (f32(atol) / scale + f32(rtol) * (r / scale).abs())
+    excess = torch.where(finite & torch.isnan(excess), scaled * scale, excess)
     worst = _worst(excess)
     if math.isnan(worst):
         return CompareResult(False, "nonfinite_error", None, None,

@@ -980,8 +980,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
                         if (g + 1 < NG) {
                             if (c == 0) {
                                 dq_init(d, g + 1);
-                                launder(d.a);
-                                launder(d.b);
+                                d.launder();
                             }
 #pragma unroll
                             for (int k = 0; k < 4; ++k)

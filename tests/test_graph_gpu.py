@@ -132,3 +132,53 @@ def test_graph_wrapper_two_live_conv_states_over_chunks():
     ga, gb = graph_caches["a"].state, graph_caches["b"].state
     assert ga.data_ptr() != gb.data_ptr()
     assert gw.stats == {"captures": 2, "replays": 2, "eager": 0}
+
+
+@pytest.mark.gpu
+def test_graphs_captured_in_separate_scopes_own_their_workspaces():
+    """Each graph_workspaces() scope (GraphWrapper opens one per capture) gets
+    scratch buffers no other scope or eager stream shares, so two captured
+    K-part projections replayed side by side on two streams each equal their
+    eager result."""
+    from autotuner_runtime import hip, ops
+    from workloads.quantize import random_quantized
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(77)
+    M, N, K = 128, 2560, 4096  # o_proj shape: the _ws entry runs K parts
+    w = [random_quantized(N, K, gen, "cuda") for _ in range(2)]
+    xs = [torch.randn((M, K), generator=gen, device="cuda").to(torch.bfloat16) for _ in range(2)]
+    rs = [torch.randn((M, N), generator=gen, device="cuda").to(torch.bfloat16) for _ in range(2)]
+    eager = [ops.qmm_residual(xs[i], *w[i], rs[i]) for i in range(2)]
+    torch.cuda.synchronize()
+
+    def capture(i):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            ops.qmm_residual(xs[i], *w[i], rs[i])
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with hip.graph_workspaces(), torch.cuda.graph(g):
+            out = ops.qmm_residual(xs[i], *w[i], rs[i])
+            ptr = hip._workspace("qmm", xs[i].device, torch.cuda.current_stream().cuda_stream,
+                                 1).data_ptr()
+        return g, out, ptr
+
+    (g0, o0, p0), (g1, o1, p1) = capture(0), capture(1)
+    eager_ptr = hip._workspace("qmm", xs[0].device, torch.cuda.current_stream().cuda_stream,
+                               1).data_ptr()
+    assert len({p0, p1, eager_ptr}) == 3
+    s0, s1 = torch.cuda.Stream(), torch.cuda.Stream()
+    for _ in range(5):
+        s0.wait_stream(torch.cuda.current_stream())
+        s1.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s0):
+            g0.replay()
+        with torch.cuda.stream(s1):
+            g1.replay()
+        torch.cuda.current_stream().wait_stream(s0)
+        torch.cuda.current_stream().wait_stream(s1)
+        torch.cuda.synchronize()
+        assert torch.equal(o0, eager[0]) and torch.equal(o1, eager[1])

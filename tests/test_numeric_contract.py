@@ -158,3 +158,17 @@ def test_max_abs_normalised_bar():
     assert not max_abs_normalised(torch.tensor([1.0, 1.0]), nan).passed
     assert max_abs_normalised(torch.zeros(3), torch.zeros(3)).passed
     assert not max_abs_normalised(torch.ones(3), torch.zeros(3)).passed
+
+
+def test_compare_evaluates_the_allowance_in_float32_like_the_reference():
+    """A value on the tolerance boundary: float32 arithmetic (the reference's
+    numeric.py:83-96) accepts it while exact arithmetic would reject it, so
+    the comparison must follow float32 here."""
+    import numpy as np
+
+    r, c, rtol = 0.612636387348175, 0.6144742965698242, 0.003
+    r32, c32 = np.float32(r), np.float32(c)
+    assert np.abs(c32 - r32) - np.float32(rtol) * np.abs(r32) <= 0       # float32: within
+    assert abs(float(c32) - float(r32)) - rtol * abs(float(r32)) > 0     # exact: outside
+    res = numeric.compare(torch.tensor([c32]), torch.tensor([r32]), rtol, 0.0)
+    assert res.passed, res
