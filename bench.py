@@ -16,7 +16,8 @@ Also measured live, with HIP events on the stream the kernels run on:
     against MI355X's dense bf16 MFMA peak (2.5 PFLOP/s);
   - qmm: the benchmark's config 2 (x[M, 2560] @ W[9728, 2560]^T, 4-bit g64) at M=1
     (HBM GB/s vs 8 TB/s) and M=128 (TFLOP/s vs the MFMA peak), rotating more
-    weight copies than the 256 MB Infinity Cache holds;
+    weight copies than the 256 MB Infinity Cache holds; beside M=1, the
+    stream floor: a read-only kernel over the same bytes and rotation;
   - lfm2_config5: the benchmark's config 5 beside the headline, the
     LFM2-1.2B-shaped hybrid prefilling 2048 tokens, 4- and 8-bit (ms per
     prefill and tok/s, one HIP-graph replay each);
@@ -151,7 +152,39 @@ def qmm_config2(torch, ops, peaks=None):
             out[f"M{M}"]["mfma_frac_measured_peak"] = round(
                 fl / us / 1e6 / peaks["mfma_bf16"]["TF_s"], 4)
     del ws
+    out["M1"]["stream_floor"] = stream_floor(torch, wbytes, copies)
     return out
+
+
+def stream_floor(torch, nbytes, copies):
+    """What the M=1 GEMV's weight bytes cost with no arithmetic: mi_peak_read
+    over `nbytes` per launch, one launch per weight-sized slice of a buffer of
+    `copies` slices (the same rotation past the Infinity Cache), in a graph,
+    best median over a few grid sizes."""
+    import measure
+
+    L = measure.peak_lib()
+    src = torch.empty(copies * nbytes, dtype=torch.uint8, device="cuda")
+    src.fill_(1)
+    best = None
+    for blocks in (304, 608, 1216, 2432):
+        sink = torch.empty(blocks, dtype=torch.int32, device="cuda")
+
+        def call(i, blocks=blocks, sink=sink):
+            st = torch.cuda.current_stream().cuda_stream
+            measure._ok(L.mi_peak_read(src.data_ptr() + (i % copies) * nbytes, nbytes, blocks,
+                                       sink.data_ptr(), st), "peak_read")
+
+        c = kernel_clock(call, 4 * copies, torch)
+        if best is None or c["median"] < best[1]["median"]:
+            best = (blocks, c)
+    del src
+    torch.cuda.empty_cache()
+    blocks, c = best
+    return {"us": round(c["median"], 2), "GB_s": round(nbytes / c["median"] / 1e3, 1),
+            "bytes": nbytes, "workgroups": blocks, "clock": spread_us(c),
+            "method": "mi_peak_read of the GEMV's weight, scale and bias bytes in a graph, "
+                      "rotating like the GEMV; best of 304-2432 workgroups"}
 
 
 def dominant_kernel(model, torch, ops, peaks=None):

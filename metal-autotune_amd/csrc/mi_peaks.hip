@@ -73,7 +73,19 @@ __global__ __launch_bounds__(PEAK_THREADS) void peak_read_kernel(const uint4 *__
 #pragma unroll
         for (int u = 0; u < PEAK_READ_UNROLL; ++u) acc ^= v[u];
     }
-    for (; i < b1; i += PEAK_THREADS) acc ^= __builtin_nontemporal_load(s + i);
+    // the tail as one predicated batch: every load is issued before the first
+    // is used, also when a workgroup's chunk is only a few loads per lane
+    // (small buffers over many workgroups)
+    if (i < b1) {
+        u32x4 v[PEAK_READ_UNROLL];
+#pragma unroll
+        for (int u = 0; u < PEAK_READ_UNROLL; ++u) {
+            const int64_t k = i + u * PEAK_THREADS;
+            v[u] = k < b1 ? __builtin_nontemporal_load(s + k) : (u32x4){0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < PEAK_READ_UNROLL; ++u) acc ^= v[u];
+    }
     uint32_t a = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
     // one word per workgroup: lanes fold by shuffle, waves through LDS
 #pragma unroll
