@@ -400,7 +400,7 @@ template <typename T, int D>
 __global__ __launch_bounds__(256) void attn_shared_kernel(
     const T *__restrict__ q, const T *__restrict__ k, const T *__restrict__ v,
     T *__restrict__ out, int64_t H, int64_t HK, int64_t Lq, int64_t Lk, int64_t cap,
-    float scale_log2, int causal, int out_layout, int quads) {
+    float scale_log2, int causal, int out_layout, int quads, int zig) {
     constexpr int KP = D + 8;  // padded K-tile row (elements)
     constexpr int DS = D / 16;
     typedef typename Vec<T>::x8 V8;
@@ -411,8 +411,21 @@ __global__ __launch_bounds__(256) void attn_shared_kernel(
     const int h2 = lane >> 5, r = lane & 31;
     unsigned bid = blockIdx.x;  // 32-bit index math, as in attn_split_kernel
     const unsigned nqb = (unsigned)ceil_div(Lq, 32);
-    const int64_t qblk = bid % nqb;
-    bid /= nqb;
+    int64_t qblk;
+    if (zig) {
+        // (nqb even) block b and b + G/2 take q blocks j and nqb - 1 - j of
+        // the same heads: under causal masking their key-tile counts add up
+        // to nqb + 1 for every pair, and a grid of two workgroups per CU
+        // places b and b + G/2 on one CU
+        const unsigned g2 = gridDim.x >> 1, hb = nqb >> 1;
+        const unsigned second = bid >= g2, u = bid - (second ? g2 : 0u);
+        const unsigned j = u % hb;
+        qblk = second ? nqb - 1 - j : j;
+        bid = u / hb;
+    } else {
+        qblk = bid % nqb;
+        bid /= nqb;
+    }
     const int quad = (int)(bid % (unsigned)quads);
     bid /= (unsigned)quads;
     const int64_t hk = bid % (unsigned)HK, b = bid / (unsigned)HK;
@@ -518,10 +531,12 @@ int launch_attn_d(const void *q, const void *k, const void *v, void *out, int64_
                   int out_layout, hipStream_t st) {
     const int quads = (int)ceil_div(H / HK, 4);
     const int64_t shared_blocks = B * HK * quads * ceil_div(Lq, 32);
+    // causal grids pair long and short q blocks (attn_shared_kernel's zig)
+    const int zig = causal && ceil_div(Lq, 32) % 2 == 0;
     if (shared_blocks >= ATT_SHARED_MIN_BLOCKS)
         attn_shared_kernel<T, D><<<(unsigned)shared_blocks, 256, 0, st>>>(
             (const T *)q, (const T *)k, (const T *)v, (T *)out, H, HK, Lq, Lk, cap, scale_log2,
-            causal, out_layout, quads);
+            causal, out_layout, quads, zig);
     else
         attn_split_kernel<T, D><<<(unsigned)(B * H * ceil_div(Lq, 32)), 64 * ATT_STREAMS, 0, st>>>(
             (const T *)q, (const T *)k, (const T *)v, (T *)out, H, HK, Lq, Lk, cap, scale_log2,
