@@ -78,7 +78,10 @@ int mi_affine_gather_dequant(const void *ids, int64_t n_ids, int ids_are_64,
  * rounding to T. Contract checks as scaffold/stitch.py:103-123. Small M runs a
  * wave-per-row GEMV with the factored per-group sum (the library's qmv regime,
  * stitch.py:176-230); larger M dequantizes in registers into bf16/fp16 MFMA
- * tiles (the qmm_t regime, stitch.py:233-293). */
+ * tiles (the qmm_t regime, stitch.py:233-293), each value T(fma(s, q, b)) as
+ * mi_affine_dequant computes it. 4-bit tiles pre-scale s by 2^24: scales of
+ * magnitude 2^104 or more (bf16 only; about 2.0e31) overflow there and give
+ * inf/NaN, where mi_affine_dequant stays finite. */
 int mi_qmm_affine(const void *x, const uint32_t *w, const void *scales, const void *biases,
                   void *y, int64_t M, int64_t N, int64_t K, int group_size, int bits,
                   int dtype, void *stream);

@@ -96,10 +96,13 @@ template <typename T> __device__ __forceinline__ uint2 pack4(const float (&f)[4]
 // 16-bit half of a word (w >> 4j) & 0x000F000F holding nibbles j and j + 4;
 // v_fma_mix_f32 reads that half as its f16 operand, so
 // fma(s * 2^24, q * 2^-24, b) = fma(s, q, b) exactly (s * 2^24 is exact for
-// every finite bf16/fp16 scale, and the kernels run with fp16 denormals
-// preserved): 19 VALU per 8 values where a byte conversion per value took
-// 23. Checked on MI355X against fmaf(s, q, b) over every finite bf16 scale,
-// all 16 nibbles and 256 biases: no difference in 484 million values.
+// every fp16 scale and every bf16 scale of magnitude below 2^104, and the
+// kernels run with fp16 denormals preserved): 19 VALU per 8 values where a
+// byte conversion per value took 23. Checked on MI355X against
+// fmaf(s, q, b) over every finite bf16 scale below 2^104, all 16 nibbles and
+// 256 biases: no difference in 484 million values. A bf16 scale of 2^104 or
+// more overflows s * 2^24 (inf, or NaN for q = 0); no quantizer produces one
+// short of weights near 3e32, and the plain dequant entry has no such limit.
 template <typename T, int BITS> struct Dequant8 {
     uint32_t r[4];  // 4 bits: the f16-denormal pairs (nibbles j, j + 4); 8 bits: w0, w1
     float s, bias;
