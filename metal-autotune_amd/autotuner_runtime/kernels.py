@@ -27,8 +27,11 @@ points own their launch geometry (tiles are chosen per shape inside the
 library), so ``grid`` / ``threadgroup`` are evaluated and validated like any
 launch expression but not passed on; specs generated for this backend leave
 them at ("1", "1", "1"), as the reference's staged specs do.
-``reference_sequence`` (an MLX op replay) and ``native_call`` (a captured
-Metal ABI) have no meaning here and are rejected at load.
+A spec with a ``reference_sequence`` (the region's recorded original MLX
+calls, a starter when no single kernel exists) replays those calls through
+the library's ops and torch (``original_sequence.prepare_sequence``), as the
+reference's LoadedKernel does (kernels.py:125-127,199-200). ``native_call``
+(a captured Metal ABI) has no meaning here and is rejected at load.
 
 Calls are stream-ordered on ``torch.cuda.current_stream()`` and never
 synchronize the host.
@@ -174,15 +177,21 @@ class LoadedKernel:
         from . import hip  # the backend; imported lazily so grammar-only use needs no GPU
 
         self.spec = spec
-        for field_name, what in (("reference_sequence", "replays MLX ops"),
-                                 ("native_call", "binds a captured Metal ABI"),
+        for field_name, what in (("native_call", "binds a captured Metal ABI"),
                                  ("atomic_outputs", "asks for Metal atomic outputs")):
             if getattr(spec, field_name) not in (None, False):
                 raise ValueError(f"kernel {spec.kernel_id}: {field_name} {what}; the HIP "
                                  "backend runs its own entry points only")
         self._stages = None
         self._entry = None
-        if spec.stages:
+        self._sequence = None
+        if spec.reference_sequence is not None:
+            if spec.stages:
+                raise ValueError(f"kernel {spec.kernel_id}: a staged region cannot also "
+                                 "replay an original sequence")
+            from .original_sequence import prepare_sequence
+            self._sequence = prepare_sequence(spec.reference_sequence)
+        elif spec.stages:
             from .stages import wiring
             reads, self._stage_outputs = wiring(spec)
             self._stages = [(LoadedKernel(st.kernel), pos) for st, pos in zip(spec.stages, reads)]
@@ -258,6 +267,8 @@ class LoadedKernel:
         if launch.fallback:
             raise ValueError(f"kernel {self.spec.kernel_id}: the fallback predicate covers "
                              "these shapes; the original ops must run them")
+        if self._sequence is not None:
+            return self._sequence(inputs)
         if self.spec.ensure_row_contiguous:
             inputs = [a.contiguous() for a in inputs]
         if self._stages is not None:

@@ -627,12 +627,17 @@ def test_sdpa(H, HK, Lq, Lk, D, causal):
 
 
 @pytest.mark.parametrize("H,HK,L,D,causal", [(32, 8, 512, 64, True), (16, 2, 1024, 128, True),
-                                             (32, 8, 512, 128, False)])
+                                             (32, 8, 512, 128, False), (32, 8, 544, 64, False)])
 def test_sdpa_shared_and_split_kernels_agree(H, HK, L, D, causal):
     """A row's attention is the same bits whichever kernel computes it. The
     L-row call runs the shared-K/V kernel (a grid of at least 128
-    workgroups); a call on its last 32 query rows, and a decode call on its
-    last row, run the key-split kernel (smaller grids) over the same keys."""
+    workgroups, causal q blocks paired long with short); a call on its last
+    32 query rows, and a decode call on its last row, run the key-split
+    kernel (smaller grids) over the same keys. Causal at head dim 64, the q
+    blocks with 1, 2, 3, 5 and 8 key tiles (fewer streams than four, streams
+    of unequal length) are also checked against split-kernel calls over
+    their own visible keys. L = 544 (17 tiles, no mask, an odd block count:
+    no pairing) gives stream 0 one tile more than the others."""
     r = rng(1050 + L + D)
     q = to_torch(oracle.round_to(r.normal(0, 1, (1, H, L, D)), "bfloat16"), "bfloat16")
     k = to_torch(oracle.round_to(r.normal(0, 1, (1, HK, L, D)), "bfloat16"), "bfloat16")
@@ -643,6 +648,14 @@ def test_sdpa_shared_and_split_kernels_agree(H, HK, L, D, causal):
     last = ops.scaled_dot_product_attention(q[:, :, L - 1:].contiguous(), k, v, D ** -0.5, mask)
     assert torch.equal(full[:, :, L - 32:], tail)
     assert torch.equal(full[:, :, L - 1:], last)
+    if causal and D == 64:
+        for j in (0, 1, 2, 4, 7):
+            rows = slice(32 * j, 32 * j + 32)
+            part = ops.scaled_dot_product_attention(q[:, :, rows].contiguous(),
+                                                    k[:, :, :32 * j + 32].contiguous(),
+                                                    v[:, :, :32 * j + 32].contiguous(),
+                                                    D ** -0.5, mask)
+            assert torch.equal(full[:, :, rows], part), f"q block {j}"
 
 
 def test_sdpa_kv_cache_capacity():
@@ -814,3 +827,55 @@ def test_determinism_three_runs():
     dev = _dev(*_quant(20, 9728, 2560), "bfloat16")
     outs = [ops.quantized_matmul(x, *dev) for _ in range(3)]
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
+
+
+def test_reference_sequence_replays_library_ops():
+    """A starter spec's recorded MLX calls replay through the library ops:
+    LFM2's conv in_proj [quantized_matmul, split(3), mul] equals the fused
+    split_gate region bit for bit (the region keeps T(B * x) of the unfused
+    projection), and [rms_norm, rope, sdpa] equals the same ops called
+    directly."""
+    from autotuner_runtime import kernels
+    from autotuner_runtime.kernels import KernelSpec
+
+    def ref(i):
+        return {"$": "ref", "i": i}
+
+    def node(op, ins, outs, *args, **kw):
+        return {"op": op, "in_arrays": ins, "out_arrays": outs,
+                "args": {"$": "tuple", "items": list(args)}, "kwargs": kw}
+
+    M, D, K = 48, 256, 512
+    r = rng(1300)
+    x = to_torch(oracle.round_to(r.normal(0, 1, (1, M, K)), "bfloat16"), "bfloat16")
+    w = _dev(*_quant(1301, 3 * D, K), "bfloat16")
+    conv_in = {"nodes": [
+        node("mx.quantized_matmul", [0, 1, 2, 3], [4], ref(0), ref(1), ref(2), ref(3),
+             transpose=True, group_size=64, bits=4),
+        node("mx.split", [4], [5, 6, 7], ref(0), 3, axis=-1),
+        node("array.__mul__", [5, 7], [8], ref(0), ref(1))],
+        "input_ids": [0, 1, 2, 3], "output_ids": [6, 8]}
+    spec = KernelSpec(kernel_id="seed_conv_in", name="seed_conv_in",
+                      input_names=("in0", "in1", "in2", "in3"), output_names=("out0", "out1"),
+                      source="// original sequence starter",
+                      output_shapes=(("1", str(M), str(D)),) * 2,
+                      output_dtypes=("bfloat16", "bfloat16"), reference_sequence=conv_in)
+    c, bx = kernels.call(spec, [x, *w])
+    fc, fbx = ops.qmm_split_gate(x, *w)
+    assert torch.equal(c, fc) and torch.equal(bx, fbx)
+
+    H, L, Dh = 4, 64, 128
+    q = to_torch(oracle.round_to(r.normal(0, 1, (1, H, L, Dh)), "bfloat16"), "bfloat16")
+    kv = to_torch(oracle.round_to(r.normal(0, 1, (1, H, L, Dh)), "bfloat16"), "bfloat16")
+    nw = to_torch(oracle.round_to(r.normal(1, 0.1, (Dh,)), "bfloat16"), "bfloat16")
+    attn = {"nodes": [
+        node("mx.fast.rms_norm", [0, 2], [3], ref(0), ref(1), 1e-6),
+        node("mx.fast.rope", [3], [4], ref(0), Dh, traditional=False, base=1e6, scale=1.0,
+             offset=0),
+        node("mx.fast.scaled_dot_product_attention", [4, 1, 1], [5], ref(0), ref(1), ref(2),
+             scale=Dh ** -0.5, mask="causal")],
+        "input_ids": [0, 1, 2], "output_ids": [5]}
+    from autotuner_runtime.original_sequence import prepare_sequence
+    (o,) = prepare_sequence(attn)([q, kv, nw])
+    qr = ops.rope(ops.rms_norm(q, nw, 1e-6), Dh, False, 1e6, 1.0, 0)
+    assert torch.equal(o, ops.scaled_dot_product_attention(qr, kv, kv, Dh ** -0.5, "causal"))

@@ -135,8 +135,7 @@ def test_unknown_entry_point_is_a_build_error():
         LoadedKernel(spec)
 
 
-@pytest.mark.parametrize("field,value", [
-    ("reference_sequence", {"ops": []}), ("native_call", {"abi": 1}), ("atomic_outputs", True)])
+@pytest.mark.parametrize("field,value", [("native_call", {"abi": 1}), ("atomic_outputs", True)])
 def test_metal_only_fields_are_rejected(stubs, field, value):
     spec = KernelSpec(**{**_double_spec().__dict__, field: value})
     with pytest.raises(ValueError):
