@@ -403,6 +403,36 @@ def test_qmm_dual_mixed_tiles_equal_plain_tiles(M, N):
         _close(sw[..., sl], oracle.swiglu(gw, uw, "bfloat16"), "bfloat16")
 
 
+@pytest.mark.parametrize("M,N", [(128, 9728), (100, 9728), (128, 10240)])
+def test_qmm_wide_single_part_tiles(M, N):
+    """A wide single-part 4-bit output at M = 128 runs 64-feature x 128-token
+    tiles (N = 9728: 152 workgroups), M = 100 the 32 x 64 grid. Tiles never
+    change results: either equals, bit for bit, rows [0, 64) and [64, M)
+    from launches of at most 64 rows, with and without the residual
+    epilogue; every element is written (NaN-filled output); and both ends
+    are within tolerance of the oracle."""
+    r = rng(880 + M + N)
+    K = 2560
+    x = oracle.round_to(r.normal(0, 1, (1, M, K)), "bfloat16")
+    q = _quant(881, N, K)
+    xd = to_torch(x, "bfloat16")
+    w = _dev(*q, "bfloat16")
+    res = to_torch(oracle.round_to(r.normal(0, 1, (1, M, N)), "bfloat16"), "bfloat16")
+    y = ops.quantized_matmul(xd, *w)
+    parts = [ops.quantized_matmul(xd[:, sl].contiguous(), *w) for sl in (slice(0, 64), slice(64, M))]
+    assert torch.equal(y, torch.cat(parts, dim=1))
+    yr = ops.qmm_residual(xd, *w, res)
+    rparts = [ops.qmm_residual(xd[:, sl].contiguous(), *w, res[:, sl].contiguous())
+              for sl in (slice(0, 64), slice(64, M))]
+    assert torch.equal(yr, torch.cat(rparts, dim=1))
+    poisoned = torch.full_like(y, float("nan"))
+    hip.b_qmm([xd, *w], [poisoned], ops._qp(64, 4))
+    assert torch.equal(poisoned, y)
+    for sl in (slice(0, 256), slice(N - 256, N)):
+        want = oracle.quantized_matmul(x, *(a[sl] for a in q), 64, 4, "bfloat16")
+        _close(y[..., sl], want, "bfloat16")
+
+
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
 def test_qmm_dual_8bit_large_tiles(dtype):
     """The 8-bit dual from M = 512 runs 128-token tiles whose x offsets are
