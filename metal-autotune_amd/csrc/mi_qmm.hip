@@ -862,12 +862,13 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
                 for (int i = 0; i < 16; ++i) acc[a][c][i] = 0.0f;
 
         // Pipeline: stage st reads the wave's slot into registers, waits for those
-        // reads, then refills the slot with stage st + 1 and computes while those
-        // DMAs fly. Every stage issues exactly OPS DMAs -- past the last stage
-        // they re-read stage nst - 1, in bounds, into the slot no later stage
-        // reads -- so at the top of a stage nothing else is in flight: vmcnt(0).
-        // The stage loop is unrolled twice so the two register weight sets are
-        // named statically.
+        // reads, then refills the slot with stage st + 1 (every stage but the
+        // last) and computes while those DMAs fly, so at the top of a stage
+        // nothing else is in flight: vmcnt(0). (Refilling past the last stage
+        // too, with a re-read of it, kept the issue pattern uniform but moved
+        // 10 % more x through a CU's L1, whose outstanding requests bound the
+        // x feed.) The stage loop is unrolled twice so the two register weight
+        // sets are named statically.
         //
         // The slot and the scale/bias table are passed as separate __restrict__
         // arguments of the inlined main loop: the resulting alias scopes let the
@@ -952,13 +953,16 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
                         launder(opa[k]);  // computed here, not sunk to its MFMA
                     }
                 }
-                const int nx = st + 1 < last ? st + 1 : last;
-                // the slot's reads have returned before its refill is issued
+                // the slot's reads have returned before its refill is issued;
+                // the last stage refills nothing (workgroup-uniform), so the
+                // loop moves each stage's x and weights exactly once
                 __builtin_amdgcn_sched_barrier(0);
                 wait_lgkmcnt0();
-                issue(nx, slot);
-                if constexpr (Sh::WREG) {  // one stage ahead, into the other set
-                    load_w(nx, wreg[(j + 1) % 2]);
+                if (st < last) {
+                    issue(st + 1, slot);
+                    if constexpr (Sh::WREG) {  // one stage ahead, into the other set
+                        load_w(st + 1, wreg[(j + 1) % 2]);
+                    }
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 // Software pipeline: each MFMA of group g is followed by a slice
@@ -997,8 +1001,8 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
         }
         };
         mainloop(xbuf, sbt);
-        // the loads issued past the last stage land before the LDS is reused for
-        // the reduction or released with the workgroup
+        // every load has landed before the LDS is reused for the reduction or
+        // released with the workgroup
         wait_vmcnt<0>();
 
         if constexpr (KM != KM_LOOP) {
