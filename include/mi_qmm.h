@@ -36,8 +36,9 @@
 extern "C" {
 #endif
 
-#define MI_ABI_VERSION 5  /* 2: mi_argmax takes a workspace; 3: mi_gelu_mlp_f32;
-                             4: mi_argmax_noalloc; 5: the qmm workspace entries */
+#define MI_ABI_VERSION 6  /* 2: mi_argmax takes a workspace; 3: mi_gelu_mlp_f32;
+                             4: mi_argmax_noalloc; 5: the qmm workspace entries;
+                             6: mi_qmm_affine_qkv_norm_rope */
 
 enum mi_dtype { MI_F32 = 0, MI_F16 = 1, MI_BF16 = 2 };
 
@@ -197,6 +198,27 @@ int mi_norm_rope_qkv(const void *q, const void *k, const void *v, int64_t q_row_
                      int64_t L, int64_t Hq, int64_t Hkv, int64_t D, float eps, int rope_dims,
                      int traditional, float base, float scale, int64_t offset, int64_t kv_cap,
                      int64_t kv_pos, int dtype, void *stream);
+
+/* The q/k/v projections and the attention prologue in one launch
+ * (patch/wrappers.py:156-176: three mx.quantized_matmul calls on the normed
+ * input, then rms_norm, transpose, rope and the cache's update_and_fetch):
+ * x [B * L, K] -> x @ dequant(w[i])^T for i = q, k, v (N = Hq D, Hkv D, Hkv D),
+ * then exactly mi_norm_rope_qkv on those three results -- q_out [B, Hq, L, D],
+ * k and v written into the caches [B, Hkv, kv_cap, D] at rows
+ * [kv_pos, kv_pos + L). Every output equals mi_qmm_affine_grouped3 followed by
+ * mi_norm_rope_qkv bit for bit; no intermediate q/k/v is written. Covers
+ * bf16/fp16 x, 4-bit weights, D = rope_dims = 128, traditional = 0, both norms, B L > 8,
+ * K % 64 == 0 and 16-byte aligned norm weights and outputs; other shapes
+ * return MI_ERR_UNSUPPORTED (launch nothing), and the caller runs the two
+ * entries instead. w, scales and biases are arrays of 3 in host memory. */
+int mi_qmm_affine_qkv_norm_rope(const void *x, const uint32_t *const w[3],
+                                const void *const scales[3], const void *const biases[3],
+                                const void *q_norm, const void *k_norm, void *q_out,
+                                void *k_cache, void *v_cache, int64_t B, int64_t L, int64_t Hq,
+                                int64_t Hkv, int64_t D, int64_t K, int group_size, int bits,
+                                float eps, int rope_dims, int traditional, float base,
+                                float scale, int64_t offset, int64_t kv_cap, int64_t kv_pos,
+                                int dtype, void *stream);
 
 /* mx.fast.scaled_dot_product_attention(q, k, v, scale, mask='causal'|None):
  * q [B, H, Lq, D]; k, v [B, HK, kv_cap, D] of which rows [0, Lk) are valid;

@@ -24,7 +24,7 @@ import torch
 
 PKG = Path(__file__).resolve().parent.parent
 LIB_PATH = Path(os.environ.get("MI_QMM_LIB", PKG / "libmiqmm.so"))
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 MI_F32, MI_F16, MI_BF16 = 0, 1, 2
 MI_OK, MI_ERR_ARG, MI_ERR_UNSUPPORTED, MI_ERR_LAUNCH = 0, 1, 2, 3
@@ -58,6 +58,9 @@ SIGNATURES: dict[str, list] = {
                      _I64, _I, _P],
     "mi_norm_rope_qkv": [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64,
                          _I64, _I64, _F, _I, _I, _F, _F, _I64, _I64, _I64, _I, _P],
+    "mi_qmm_affine_qkv_norm_rope": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                                    _I64, _I64, _I, _I, _F, _I, _I, _F, _F, _I64, _I64, _I64,
+                                    _I, _P],
     "mi_sdpa": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _I, _P],
     "mi_swiglu": [_P, _P, _P, _I64, _I, _P],
     "mi_shortconv": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I, _P],

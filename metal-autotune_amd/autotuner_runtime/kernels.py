@@ -301,6 +301,12 @@ def _covered_call(spec, inputs, sized: bool, init_value):
     return lk(inputs, init_value=init_value, launch=plan)
 
 
+def covers_sized(spec: KernelSpec, inputs: list[torch.Tensor]) -> bool:
+    """Whether ``try_sized(spec, inputs)`` would launch the region (not decline
+    it to the original ops)."""
+    return not _kernel_for(spec).launch(inputs, checked_elsewhere=True).fallback
+
+
 def fallback_fires(spec: KernelSpec, inputs: list[torch.Tensor]) -> bool:
     """Whether the region's original ops must run these inputs."""
     return _kernel_for(spec).fallback_fires(inputs)

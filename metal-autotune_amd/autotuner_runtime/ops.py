@@ -10,6 +10,7 @@ tensors (hip.lib() raises otherwise); there is no CPU path.
 
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
@@ -170,6 +171,53 @@ def norm_rope_qkv(q, k, v, q_norm, k_norm, n_heads: int, n_kv_heads: int, eps: f
         v_cache.data_ptr(), B, L, n_heads, n_kv_heads, D, float(eps), int(dims),
         int(traditional), float(base), float(scale), int(offset), k_cache.shape[2],
         int(cache_pos), hip._dt(q), hip._stream(q)), "norm_rope_qkv")
+    return out
+
+
+def qkv_norm_rope(x, weights, q_norm, k_norm, n_heads: int, n_kv_heads: int, eps: float,
+                  dims: int, base: float, offset: int, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, cache_pos: int, group_size: int = 64, bits: int = 4,
+                  traditional: bool = False, scale: float = 1.0) -> torch.Tensor | None:
+    """The q/k/v projections and the attention prologue in one launch:
+    ``norm_rope_qkv(*qmm_grouped3(x, weights), ...)`` bit for bit, without
+    writing q, k and v (patch/wrappers.py:156-176). ``weights`` is the (w,
+    scales, biases) triples of q, k and v. Returns q_out [B, Hq, L, D] (k and v
+    go into the caches at rows [cache_pos, cache_pos + L)), or None when the
+    fused entry does not cover these shapes -- the caller then runs the two
+    ops."""
+    if x.dim() != 3:
+        raise ValueError(f"x must be [B, L, K], got {tuple(x.shape)}")
+    B, L, _ = x.shape
+    p = _qp(group_size, bits)
+    Ns = [hip._qmm_dims(x, w, s, b, p)[1] for w, s, b in weights]
+    if Ns[0] % n_heads or Ns[1] % n_kv_heads or Ns[2] != Ns[1]:
+        raise ValueError(f"projection widths {Ns} do not split into {n_heads} / {n_kv_heads} heads")
+    D = Ns[0] // n_heads
+    if Ns[1] // n_kv_heads != D:
+        raise ValueError("q and k/v heads must share a head dim")
+    for c in (k_cache, v_cache):
+        if (not c.is_contiguous() or c.dim() != 4 or c.shape[0] != B
+                or c.shape[1] != n_kv_heads or c.shape[3] != D or c.dtype != x.dtype):
+            raise ValueError(f"cache {tuple(c.shape)} does not hold {(B, n_kv_heads, '*', D)}")
+    for wt in (q_norm, k_norm):
+        if tuple(wt.shape) != (D,) or wt.dtype != x.dtype or not wt.is_contiguous():
+            raise ValueError(f"norm weight must be contiguous {x.dtype} [{D}]")
+    hip._require_gpu(x)
+    x = x.contiguous()
+    hip._contig(*[t for triple in weights for t in triple])
+    dt = hip._act_dtype(x, weights[0][1])
+    out = _empty((B, n_heads, L, D), x)
+    ptrs = ctypes.c_void_p * 3
+    status = hip.lib().mi_qmm_affine_qkv_norm_rope(
+        x.data_ptr(), ptrs(*[w.data_ptr() for w, _, _ in weights]),
+        ptrs(*[s.data_ptr() for _, s, _ in weights]), ptrs(*[b.data_ptr() for _, _, b in weights]),
+        q_norm.data_ptr(), k_norm.data_ptr(), out.data_ptr(), k_cache.data_ptr(),
+        v_cache.data_ptr(), B, L, n_heads, n_kv_heads, D, x.shape[-1], group_size, bits,
+        float(eps), int(dims), int(traditional), float(base), float(scale), int(offset),
+        k_cache.shape[2], int(cache_pos), dt, hip._stream(x))
+    if status == hip.MI_ERR_UNSUPPORTED:
+        return None
+    hip._check(status, "qkv_norm_rope")
     return out
 
 

@@ -115,6 +115,17 @@ class SizedRegions(ReplayWrapper):
             return None
         return _kernels.try_sized(spec, inputs)
 
+    def _serves(self, role: str, inputs, n: int) -> bool:
+        """Whether ``self._try(role, inputs, n)`` would launch the role's kernel
+        (for a caller that runs a fused form of the same cut in its place)."""
+        spec = self._specs.get(role)
+        if spec is None:
+            return False
+        ranges = self.__dict__.get("_ranges", type(self).RANGES)
+        if ranges is not None and not in_runs(n, ranges.get(spec.kernel_id, ())):
+            return False
+        return _kernels.covers_sized(spec, inputs)
+
     def set_ranges(self, ranges: dict | None) -> None:
         object.__setattr__(self, "_ranges", ranges)
 

@@ -32,6 +32,17 @@ template <typename T> __device__ __forceinline__ float f32(T v) { return (float)
 // v_cvt_f16_f32 on gfx950).
 template <typename T> __device__ __forceinline__ T cvt(float v) { return (T)v; }
 
+// An fp32 result held as fp32 before a conversion to T, as the source writes
+// it. For fp16 the compiler otherwise folds the product or fma that makes v
+// into one mixed-precision instruction (v_fma_mixlo_f16) that rounds once,
+// straight to fp16: a different value in a few last places, chosen or not
+// depending on the surrounding code -- so two kernels that share an
+// expression could disagree. (bf16 has no such instruction.)
+template <typename T> __device__ __forceinline__ float pin32(float v) {
+    if constexpr (sizeof(T) == 2 && !__is_same(T, bf16)) asm volatile("" : "+v"(v));
+    return v;
+}
+
 __device__ __forceinline__ uint4 ld16(const void *p) { return *(const uint4 *)p; }
 // A 16-byte load marked non-temporal (streamed data read once: quantized
 // weights in the GEMV). Measured on MI355X over a 2 GiB read: 7.0-7.1 TB/s
@@ -163,6 +174,16 @@ __device__ __forceinline__ void launder(uint4 &v) {
     asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
 }
 __device__ __forceinline__ void launder(uint32_t &v) { asm volatile("" : "+v"(v)); }
+
+// The rotation of a pair (a, c) by an angle of cosine cs and sine sn, each
+// output one fma over a rounded product: a cs - c sn and a sn + c cs
+// (norm_rope_kernel and the q/k/v GEMM's head epilogue share them).
+__device__ __forceinline__ float rope_first(float a, float c, float cs, float sn) {
+    return __builtin_fmaf(a, cs, -(c * sn));
+}
+__device__ __forceinline__ float rope_second(float a, float c, float cs, float sn) {
+    return __builtin_fmaf(a, sn, c * cs);
+}
 
 __host__ __device__ constexpr int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

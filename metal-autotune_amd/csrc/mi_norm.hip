@@ -57,13 +57,13 @@ __global__ __launch_bounds__(256) void rms_kernel(const T *__restrict__ x, const
                 unpack8<T>(ld16(xr + 8 * c), f);
                 unpack8<T>(ld16(w + 8 * c), g);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) f[i] = g[i] * (float)cvt<T>(f[i] * inv);
+                for (int i = 0; i < 8; ++i) f[i] = g[i] * (float)cvt<T>(pin32<T>(f[i] * inv));
                 st16(yr + 8 * c, pack8<T>(f));
             }
         }
     } else {
         for (int64_t k = lane; k < D; k += 64)
-            yr[k] = cvt<T>((float)w[k] * (float)cvt<T>((float)xr[k] * inv));
+            yr[k] = cvt<T>((float)w[k] * (float)cvt<T>(pin32<T>((float)xr[k] * inv)));
     }
 }
 
@@ -104,7 +104,7 @@ __device__ __forceinline__ void rms_row_store(const uint4 (&xv)[RMS_RC],
             unpack8<T>(xv[i], f);
             unpack8<T>(wv[i], g);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) f[e] = g[e] * (float)cvt<T>(f[e] * inv);
+            for (int e = 0; e < 8; ++e) f[e] = g[e] * (float)cvt<T>(pin32<T>(f[e] * inv));
             st16(yr + 8 * c, pack8<T>(f));
         }
     }
@@ -179,7 +179,7 @@ __global__ __launch_bounds__(256) void rms_parts_kernel(const float *__restrict_
         float f[8];
         unpack8<T>(rv[i], f);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) f[e] = f[e] + (float)cvt<T>(s[e]);
+        for (int e = 0; e < 8; ++e) f[e] = pin32<T>(f[e] + (float)cvt<T>(s[e]));
         xv[i] = pack8<T>(f);
         if (c < nc) st16(h + row * D + 8 * c, xv[i]);
     }
@@ -225,15 +225,6 @@ struct NRJobs {
     NRJob j0, j1, j2;
     int64_t end0, end1, rows;  // cumulative row ends
 };
-
-// The rotation of a pair (a, c) by an angle of cosine cs and sine sn, each
-// output one fma over a rounded product: a cs - c sn and a sn + c cs.
-__device__ __forceinline__ float rope_first(float a, float c, float cs, float sn) {
-    return __builtin_fmaf(a, cs, -(c * sn));
-}
-__device__ __forceinline__ float rope_second(float a, float c, float cs, float sn) {
-    return __builtin_fmaf(a, sn, c * cs);
-}
 
 // R lanes per row. VEC (16-bit T, D == 8 R, every row 16-byte aligned): each
 // lane owns four rotation pairs (elements 4t..4t+3 and their partners D/2
@@ -299,15 +290,15 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NRJobs jobs, int64_t B, 
                 unpack4<T>(wc, gc);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    a[e] = (float)cvt<T>(ga[e] * (float)cvt<T>(a[e] * inv));
-                    c[e] = (float)cvt<T>(gc[e] * (float)cvt<T>(c[e] * inv));
+                    a[e] = (float)cvt<T>(ga[e] * (float)cvt<T>(pin32<T>(a[e] * inv)));
+                    c[e] = (float)cvt<T>(gc[e] * (float)cvt<T>(pin32<T>(c[e] * inv)));
                 }
             }
             float r0[4], r1[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                r0[e] = rope_first(a[e], c[e], cs[e], sn[e]);
-                r1[e] = rope_second(a[e], c[e], cs[e], sn[e]);
+                r0[e] = pin32<T>(rope_first(a[e], c[e], cs[e], sn[e]));
+                r1[e] = pin32<T>(rope_second(a[e], c[e], cs[e], sn[e]));
             }
             st8(orow + e0, pack4<T>(r0));
             st8(orow + hd + e0, pack4<T>(r1));
@@ -330,7 +321,7 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NRJobs jobs, int64_t B, 
             for (int o = R / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, R);
             const float inv = 1.0f / __fsqrt_rn(ss / (float)D + eps);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) f[e] = (float)cvt<T>(g[e] * (float)cvt<T>(f[e] * inv));
+            for (int e = 0; e < 8; ++e) f[e] = (float)cvt<T>(g[e] * (float)cvt<T>(pin32<T>(f[e] * inv)));
             st16(orow + 8 * t, pack8<T>(f));
             return;
         }
@@ -352,11 +343,11 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NRJobs jobs, int64_t B, 
 #pragma unroll
             for (int o = R / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, R);
             const float inv = 1.0f / __fsqrt_rn(ss / (float)D + eps);
-            a = (float)cvt<T>(wa * (float)cvt<T>(a0 * inv));
-            c = (float)cvt<T>(wc * (float)cvt<T>(c0 * inv));
+            a = (float)cvt<T>(wa * (float)cvt<T>(pin32<T>(a0 * inv)));
+            c = (float)cvt<T>(wc * (float)cvt<T>(pin32<T>(c0 * inv)));
         }
-        orow[t] = cvt<T>(rope_first(a, c, cs, sn));
-        orow[t + R] = cvt<T>(rope_second(a, c, cs, sn));
+        orow[t] = cvt<T>(pin32<T>(rope_first(a, c, cs, sn)));
+        orow[t + R] = cvt<T>(pin32<T>(rope_second(a, c, cs, sn)));
         return;
     }
     float inv = 1.0f;
@@ -382,15 +373,15 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(NRJobs jobs, int64_t B, 
         }
         float a = (float)xr[e0], c = (float)xr[e1];
         if (w) {
-            a = (float)cvt<T>((float)w[e0] * (float)cvt<T>(a * inv));
-            c = (float)cvt<T>((float)w[e1] * (float)cvt<T>(c * inv));
+            a = (float)cvt<T>((float)w[e0] * (float)cvt<T>(pin32<T>(a * inv)));
+            c = (float)cvt<T>((float)w[e1] * (float)cvt<T>(pin32<T>(c * inv)));
         }
         if (rot) {
             const float inv_freq = exp2f(-(float)(2 * p) / (float)dims * log2base);
             float sn, cs;
             sincosf(position * inv_freq, &sn, &cs);
-            const float ra = rope_first(a, c, cs, sn);
-            const float rc = rope_second(a, c, cs, sn);
+            const float ra = pin32<T>(rope_first(a, c, cs, sn));
+            const float rc = pin32<T>(rope_second(a, c, cs, sn));
             a = ra;
             c = rc;
         }

@@ -26,14 +26,19 @@
 // Epilogues implement the reference's region cuts: plain store; [qmm, add];
 // [qmm, split(3), mul]; [qmm(w1), qmm(w3)] (two outputs, or swiglu fused);
 // and three projections sharing x in one launch (EPI_GROUP3: the weights and
-// outputs are concatenated along N and each workgroup's tile lies in one part).
+// outputs are concatenated along N and each workgroup's tile lies in one part);
+// the same three projections with the attention prologue fused (EPI_HEADNR:
+// each workgroup owns one 128-value head of q, k or v for 32 tokens and applies
+// the q/k RMSNorm, RoPE and the transposed cache write to its sums).
+#include <math.h>
+
 #include "mi_common.h"
 
 namespace mi {
 namespace {
 
 enum Epi { EPI_STORE = 0, EPI_RESID = 1, EPI_SPLIT3 = 2, EPI_DUAL = 3, EPI_SWIGLU = 4,
-           EPI_GROUP3 = 5 };
+           EPI_GROUP3 = 5, EPI_HEADNR = 6 };
 
 // weight rows each output element combines (EPI_GROUP3 selects one weight per tile)
 constexpr int epi_parts(int e) {
@@ -62,6 +67,13 @@ struct QParams {
     int ks;                    // K parts (kpart_count): each is split over the wk waves
     int kslice;                // k values of the longest wave chunk (ks * wk chunks of K)
     float *part;               // non-null: write K part blockIdx.z's sums, fp32 [ks, M, Nout]
+    // EPI_HEADNR (the parts are q, k, v; py[] = q_out [B, Hq, L, D], k_cache,
+    // v_cache [B, Hkv, cap, D]; D = 128)
+    const void *nw[2];         // q_norm, k_norm: T [D]
+    int64_t L;                 // tokens per sequence (M = B L)
+    int64_t cap, pos0;         // cache rows per head; first row written
+    int64_t offset;            // RoPE position of a sequence's token 0
+    float eps, log2base, rscale;
 };
 
 // K parts of the MFMA path: a function of (M, K) alone, so every entry point
@@ -96,6 +108,7 @@ struct Bound {
     int64_t o0, o1, o2;  // row offset of each part inside its weight
     void *y0;            // this workgroup's output
     int64_t Nout;        // its width
+    int gp;              // EPI_GROUP3 / EPI_HEADNR: the part it lies in
     __device__ const uint32_t *w(int i) const { return i == 0 ? w0 : (i == 1 ? w1 : w2); }
     __device__ const void *s(int i) const { return i == 0 ? s0 : (i == 1 ? s1 : s2); }
     __device__ const void *b(int i) const { return i == 0 ? b0 : (i == 1 ? b1 : b2); }
@@ -109,8 +122,8 @@ struct Bound {
 template <int EPI>
 __device__ __forceinline__ Bound bind(const QParams &p, int64_t &nb) {
     Bound q = {p.w[0], p.w[1], p.w[2], p.s[0], p.s[1], p.s[2], p.b[0], p.b[1], p.b[2],
-               p.noff[0], p.noff[1], p.noff[2], p.y0, p.Nout};
-    if constexpr (EPI == EPI_GROUP3) {
+               p.noff[0], p.noff[1], p.noff[2], p.y0, p.Nout, 0};
+    if constexpr (EPI == EPI_GROUP3 || EPI == EPI_HEADNR) {
         const int64_t e0 = p.pn[0], e1 = p.pn[0] + p.pn[1];
         const bool p0 = nb < e0, p1 = !p0 && nb < e1;
         nb -= p0 ? 0 : (p1 ? e0 : e1);
@@ -119,6 +132,7 @@ __device__ __forceinline__ Bound bind(const QParams &p, int64_t &nb) {
         q.b0 = p0 ? p.b[0] : (p1 ? p.b[1] : p.b[2]);
         q.y0 = p0 ? p.py[0] : (p1 ? p.py[1] : p.py[2]);
         q.Nout = p0 ? p.pn[0] : (p1 ? p.pn[1] : p.pn[2]);
+        q.gp = p0 ? 0 : (p1 ? 1 : 2);
     }
     return q;
 }
@@ -129,10 +143,10 @@ __device__ __forceinline__ void epi1(const QParams &p, const Bound &bd, int64_t 
                                      const float *acc) {
     T *y0 = (T *)bd.y0;
     const int64_t o = m * bd.Nout + n;
-    if constexpr (EPI == EPI_STORE || EPI == EPI_GROUP3) {
+    if constexpr (EPI == EPI_STORE || EPI == EPI_GROUP3 || EPI == EPI_HEADNR) {
         y0[o] = cvt<T>(acc[0]);
     } else if constexpr (EPI == EPI_RESID) {
-        y0[o] = cvt<T>((float)((const T *)p.resid)[o] + (float)cvt<T>(acc[0]));
+        y0[o] = cvt<T>(pin32<T>((float)((const T *)p.resid)[o] + (float)cvt<T>(acc[0])));
     } else if constexpr (EPI == EPI_SPLIT3) {
         // split(3): parts 0, 1, 2 are B, C, x; outputs C and T(B * x)
         y0[o] = cvt<T>(acc[1]);
@@ -176,7 +190,7 @@ __device__ __forceinline__ void epi4(const QParams &p, const Bound &bd, int64_t 
     }
     const int64_t o = m * bd.Nout + n;
     float v[4];
-    if constexpr (EPI == EPI_STORE || EPI == EPI_GROUP3) {
+    if constexpr (EPI == EPI_STORE || EPI == EPI_GROUP3 || EPI == EPI_HEADNR) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = acc[0][e];
     } else if constexpr (EPI == EPI_RESID) {
@@ -184,7 +198,7 @@ __device__ __forceinline__ void epi4(const QParams &p, const Bound &bd, int64_t 
         typedef typename Vec<T>::x4 V4;
         const V4 rv = __builtin_bit_cast(V4, rr);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (float)rv[e] + (float)cvt<T>(acc[0][e]);
+        for (int e = 0; e < 4; ++e) v[e] = pin32<T>((float)rv[e] + (float)cvt<T>(acc[0][e]));
     } else if constexpr (EPI == EPI_SPLIT3) {
         float bx[4];
 #pragma unroll
@@ -666,9 +680,96 @@ __device__ __forceinline__ void wait_lgkmcnt0() {
 // so three workgroups of four waves share a CU (at most 168 registers a
 // lane), which tiles of up to four 32x32 accumulators fit without spilling;
 // larger tiles, and 128-token tiles (whose slot alone leaves room for two
-// workgroups), ask for two (256 registers).
-template <int A, int C> constexpr int mfma_waves_per_eu() {
-    return A * C <= 4 && C <= 2 ? 3 : 2;
+// workgroups), ask for two (256 registers). So do the whole-head tiles of
+// EPI_HEADNR, whose RoPE angles stay in registers through the loop (at the
+// Qwen3 prefill size they fill 192 CUs with one workgroup each).
+template <int A, int C, int EPI = 0> constexpr int mfma_waves_per_eu() {
+    return A * C <= 4 && C <= 2 && EPI != EPI_HEADNR ? 3 : 2;
+}
+
+// EPI_HEADNR epilogue. The workgroup's tile is head n_head / 128 of part
+// bd.gp (0 q, 1 k, 2 v) for tokens m_blk .. m_blk + 31; after the K-split
+// reduction wave q holds features 32 a + 8 q + 4 h + e (a, e < 4) of token
+// m_blk + r in acc[a][e]. The arithmetic is norm_rope_kernel's 16-lane form
+// on the T-rounded sums, which a separate launch would read back: there lane t
+// owns features 4t .. 4t+3 and their RoPE partners 64 + 4t .., sums their
+// squares in one fma chain (its four, then the partners) and adds the 16
+// lanes' sums in an xor butterfly (8, 4, 2, 1). Here a lane holds t = 2q + h
+// (a = 0 with its partners a = 2) and t + 8 (a = 1 with a = 3): butterfly
+// level 8 is an add in the lane, and levels 4, 2 and 1 pair the token's eight
+// level-8 sums the same way after an exchange through xch (8 x 32 floats of
+// LDS). A two-operand add commutes exactly, so the sum, and every output,
+// equals the separate launch's bit for bit. sn and cs are the sine and cosine
+// of the rotation of pair (f, f + 64), f = 32 a + 8 q + 4 h + e (a < 2),
+// from the separate launch's expressions (computed in the tile's prologue).
+template <typename T>
+__device__ __forceinline__ void head_norm_rope(const QParams &p, const Bound &bd,
+                                               const float (&acc)[4][4], const float (&sn)[2][4],
+                                               const float (&cs)[2][4], int q, int h, int r,
+                                               int64_t m_blk, int64_t n_head, float *xch) {
+    constexpr int D = 128;
+    const int64_t m = m_blk + r;
+    const bool live = m < p.M;
+    const int64_t mm = live ? m : p.M - 1;  // (tokens past M store nothing)
+    const int64_t l = mm % p.L, b = mm / p.L;
+    const int part = bd.gp;  // workgroup-uniform
+    const int64_t H = bd.Nout / D, hd = n_head / D;
+    const int64_t cap = part == 0 ? p.L : p.cap, pos0 = part == 0 ? 0 : p.pos0;
+    T *orow = (T *)bd.y0 + ((b * H + hd) * cap + pos0 + l) * D;
+    const int f0 = 8 * q + 4 * h;  // the lane's first feature in each 32-feature tile
+    float v[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[a][e] = (float)cvt<T>(acc[a][e]);
+    if (part == 2) {  // v: the cache rows as the GEMM rounds them
+        if (live) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a) st8(orow + 32 * a + f0, pack4<T>(v[a]));
+        }
+        return;
+    }
+    float s0 = 0.0f, s1 = 0.0f;  // the separate launch's lanes t = 2q + h and t + 8
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s0 = __builtin_fmaf(v[0][e], v[0][e], s0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s0 = __builtin_fmaf(v[2][e], v[2][e], s0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s1 = __builtin_fmaf(v[1][e], v[1][e], s1);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s1 = __builtin_fmaf(v[3][e], v[3][e], s1);
+    xch[(2 * q + h) * 32 + r] = s0 + s1;  // level 8
+    __syncthreads();
+    float x1[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) x1[t] = xch[t * 32 + r];
+    // level 4 pairs t with t ^ 4, level 2 with t ^ 2, level 1 with t ^ 1
+    const float ss = ((x1[0] + x1[4]) + (x1[2] + x1[6])) + ((x1[1] + x1[5]) + (x1[3] + x1[7]));
+    const float inv = 1.0f / __fsqrt_rn(ss / (float)D + p.eps);
+    const T *w = (const T *)p.nw[part];
+    float g[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) unpack4<T>(ld8(w + 32 * a + f0), g[a]);
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            v[a][e] = (float)cvt<T>(g[a][e] * (float)cvt<T>(pin32<T>(v[a][e] * inv)));
+    float r0[2][4], r1[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {  // the pair (f, f + 64), f = 32 a + f0 + e
+            r0[a][e] = pin32<T>(rope_first(v[a][e], v[a + 2][e], cs[a][e], sn[a][e]));
+            r1[a][e] = pin32<T>(rope_second(v[a][e], v[a + 2][e], cs[a][e], sn[a][e]));
+        }
+    if (live) {
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            st8(orow + 32 * a + f0, pack4<T>(r0[a]));
+            st8(orow + 64 + 32 * a + f0, pack4<T>(r1[a]));
+        }
+    }
 }
 
 // One workgroup's tile: tokens [m_blk, m_blk + 32 * C) of the output features
@@ -776,6 +877,25 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
     }
     const uint32_t xrows8 = (uint32_t)(8 * K * (int64_t)sizeof(T));  // 8 token rows in bytes
     f32x16 acc[A][C];
+    // EPI_HEADNR: the RoPE angles of the lane's eight rotation pairs (see
+    // head_norm_rope), computed while the first stage's loads are in flight
+    float hsn[2][4], hcs[2][4];
+    auto head_angles = [&]() {
+        if constexpr (EPI == EPI_HEADNR) {
+            const int64_t m = m_blk + r < p.M ? m_blk + r : p.M - 1;
+            const float position = (float)(m % p.L + p.offset) * p.rscale;
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int f = 32 * a + 8 * kw + 4 * h + e;
+                    const float inv_freq = exp2f(-(float)(2 * f) / 128.0f * p.log2base);
+                    sincosf(position * inv_freq, &hsn[a][e], &hcs[a][e]);
+                    // kept here, under the loads' latency, not sunk to the epilogue
+                    asm volatile("" : "+v"(hsn[a][e]), "+v"(hcs[a][e]));
+                }
+        }
+    };
     for (int kp = 0; kp < nparts; ++kp) {  // workgroup-uniform
         const int cix = (KM == KM_PART ? kz : kp) * wk + kw;
         const int sbeg = (cix * nstages) >> cshift;
@@ -897,6 +1017,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
         };
         issue(0, slot);
         if constexpr (Sh::WREG) load_w(0, wreg[0]);
+        head_angles();
         // the table's DMAs were issued before the prologue's
         wait_vmcnt<Sh::TABLE_VMCNT>();
         load_sb(0);
@@ -1078,6 +1199,19 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
                             }
                     }
                 }
+                if constexpr (EPI == EPI_HEADNR) {
+                    static_assert(A == 4 && C == 1 && KM == KM_ONE, "one 128-value head, 32 tokens");
+                    float hv[4][4];
+#pragma unroll
+                    for (int a = 0; a < 4; ++a)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) hv[a][e] = acc[a][0][e];
+                    // the scale/bias tables are no longer read (the reduction's
+                    // first barrier follows every wave's last stage)
+                    head_norm_rope<T>(p, bd, hv, hsn, hcs, kw, h, r, m_blk, n_wave,
+                                      (float *)lds_dyn);
+                    return;
+                }
                 const int blk = kw;  // this wave's quarter
                 if constexpr (KM == KM_PART) {
                     float *dst = p.part + (int64_t)kz * p.M * bd.Nout;
@@ -1242,7 +1376,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
 
 template <typename T, int BITS, int A, int C, int WK, int EPI, int KM>
 __global__ __launch_bounds__(64 * WK)
-__attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<A, C>()))) void qmm_mfma_kernel(
+__attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<A, C, EPI>()))) void qmm_mfma_kernel(
     QParams p) {
     constexpr int TN = (epi_parts(EPI) == 1) ? A : 1;
     __shared__ __attribute__((aligned(16))) char lds[MfmaShape<T, BITS, A, C, WK>::LDS];
@@ -1644,7 +1778,7 @@ __global__ __launch_bounds__(256) void qmm_parts_sum_kernel(QParams p) {
         typedef typename Vec<T>::x4 V4;
         const V4 rv = __builtin_bit_cast(V4, rr);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = (float)rv[e] + (float)cvt<T>(s[e]);
+        for (int e = 0; e < 4; ++e) y[e] = pin32<T>((float)rv[e] + (float)cvt<T>(s[e]));
     } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e) y[e] = s[e];
@@ -1885,4 +2019,77 @@ extern "C" int mi_qmm_affine_grouped3(const void *x, const uint32_t *const w[3],
         p.pn[i] = N[i];
     }
     return run<EPI_GROUP3>(p, bits, dtype, stream);
+}
+
+namespace mi {
+namespace {
+
+// Whole-head tiles: 128 features (four 32-feature tiles a wave) by 32 tokens,
+// four K-split waves.
+template <typename T, int BITS>
+int launch_headnr(const QParams &p, hipStream_t st) {
+    return launch_mfma_cfg<T, BITS, 4, 1, EPI_HEADNR>(p, 4, st);
+}
+
+}  // namespace
+}  // namespace mi
+
+extern "C" int mi_qmm_affine_qkv_norm_rope(
+    const void *x, const uint32_t *const w[3], const void *const scales[3],
+    const void *const biases[3], const void *q_norm, const void *k_norm, void *q_out,
+    void *k_cache, void *v_cache, int64_t B, int64_t L, int64_t Hq, int64_t Hkv, int64_t D,
+    int64_t K, int group_size, int bits, float eps, int rope_dims, int traditional, float base,
+    float scale, int64_t offset, int64_t kv_cap, int64_t kv_pos, int dtype, void *stream) {
+    if (!w || !scales || !biases) return fail(MI_ERR_ARG, "null array argument");
+    if (B < 0 || L < 0 || Hq <= 0 || Hkv <= 0 || D <= 0)
+        return fail(MI_ERR_ARG, "qkv shape B=%lld L=%lld Hq=%lld Hkv=%lld D=%lld", (long long)B,
+                    (long long)L, (long long)Hq, (long long)Hkv, (long long)D);
+    const int64_t M = B * L;
+    const int64_t N[3] = {Hq * D, Hkv * D, Hkv * D};
+    void *const y[3] = {q_out, k_cache, v_cache};
+    for (int i = 0; i < 3; ++i)
+        if (int e = check_common(x, w[i], scales[i], biases[i], y[i], M, N[i], K, group_size,
+                                 bits, dtype))
+            return e;
+    if (kv_pos < 0 || kv_pos + L > kv_cap)
+        return fail(MI_ERR_ARG, "rows [%lld, %lld) exceed the cache capacity %lld",
+                    (long long)kv_pos, (long long)(kv_pos + L), (long long)kv_cap);
+    if (!(base > 0.0f)) return fail(MI_ERR_ARG, "rope base must be positive");
+    // The fused form covers 16-bit heads of 128 values rotated whole (not
+    // traditional), both norms, the MFMA path's shapes, and 16-byte aligned
+    // norm weights and outputs (the layout under which the separate launch
+    // takes the 16-lane form whose arithmetic the epilogue repeats).
+    // (4-bit weights: the 8-bit whole-head tile spills at three waves a SIMD)
+    if (dtype == MI_F32 || bits != 4 || D != 128 || rope_dims != 128 || traditional || !q_norm ||
+        !k_norm)
+        return fail(MI_ERR_UNSUPPORTED, "fused q/k/v + norm + rope covers 16-bit, 4-bit weights, "
+                                        "D = rope dims = 128, both norms");
+    if (!mfma_shape_ok(M, K, N[0], group_size, bits) ||
+        !mfma_shape_ok(M, K, N[1], group_size, bits))
+        return fail(MI_ERR_UNSUPPORTED, "fused q/k/v + norm + rope: M=%lld K=%lld off the MFMA path",
+                    (long long)M, (long long)K);
+    if (!aligned(q_norm, 16) || !aligned(k_norm, 16) || !aligned(q_out, 16) ||
+        !aligned(k_cache, 16) || !aligned(v_cache, 16))
+        return fail(MI_ERR_UNSUPPORTED, "fused q/k/v + norm + rope needs 16-byte aligned rows");
+    if (M == 0) return MI_OK;
+    QParams p = base_params(x, w[0], scales[0], biases[0], q_out, M, N[0] + N[1] + N[2], K,
+                            group_size);
+    for (int i = 0; i < 3; ++i) {
+        p.w[i] = w[i];
+        p.s[i] = scales[i];
+        p.b[i] = biases[i];
+        p.py[i] = y[i];
+        p.pn[i] = N[i];
+    }
+    p.nw[0] = q_norm;
+    p.nw[1] = k_norm;
+    p.L = L;
+    p.cap = kv_cap;
+    p.pos0 = kv_pos;
+    p.offset = offset;
+    p.eps = eps;
+    p.log2base = (float)log2((double)base);
+    p.rscale = scale;
+    hipStream_t st = as_stream(stream);
+    return dtype == MI_BF16 ? launch_headnr<bf16, 4>(p, st) : launch_headnr<f16, 4>(p, st);
 }

@@ -17,7 +17,12 @@ fallback predicate fires (patch/wrappers.py:51-55 pattern):
   [qmm(o_proj), add, rms_norm(post_attention_layernorm)] -> residual_rmsnorm
   [qmm(gate), qmm(up), swiglu]                           -> dual_swiglu
   [qmm(down), add]                                       -> residual
-  reshape -> q_norm/k_norm -> transpose -> rope (+cache)  -> norm_rope
+  [qmm(q), qmm(k), qmm(v)]                               -> qkv (grouped3)
+  reshape -> q_norm/k_norm -> transpose -> rope (+cache)  -> norm_rope_qkv
+
+Where the qkv cut serves the call, the two last rows run as one launch
+(``ops.qkv_norm_rope``: the prologue in the GEMM's epilogue, the same bits);
+shapes the fused entry does not take run them as two.
 
 ``install_regions`` also links neighbouring layers: layer i's last cut
 becomes [qmm(down), add, rms_norm(layer i+1's input_layernorm)], the same
@@ -244,14 +249,24 @@ class Qwen3LayerRegions(SizedRegions):
         if xn is None:
             xn = w.input_layernorm(x)
         projs = (attn.q_proj, attn.k_proj, attn.v_proj)
-        outs = self._try("qkv", [xn] + [t for m in projs for t in (m.weight, m.scales, m.biases)],
-                         L)
-        q, k, v = (m(xn) for m in projs) if outs is None else outs
-        # q/k-norm + RoPE + the KV-cache update, one launch
-        qr = ops.norm_rope_qkv(q, k, v, attn.q_norm.weight, attn.k_norm.weight,
-                               c.num_attention_heads, c.num_key_value_heads, c.rms_norm_eps,
-                               c.head_dim, c.rope_theta, cache.offset, cache.keys, cache.values,
-                               cache.offset)
+        ins = [xn] + [t for m in projs for t in (m.weight, m.scales, m.biases)]
+        qr = None
+        if self._serves("qkv", ins, L):
+            # the q/k/v cut with the prologue below in its epilogue, the same
+            # bits (None: shapes the fused entry does not take)
+            qr = ops.qkv_norm_rope(xn, [(m.weight, m.scales, m.biases) for m in projs],
+                                   attn.q_norm.weight, attn.k_norm.weight, c.num_attention_heads,
+                                   c.num_key_value_heads, c.rms_norm_eps, c.head_dim,
+                                   c.rope_theta, cache.offset, cache.keys, cache.values,
+                                   cache.offset, c.group_size, c.bits)
+        if qr is None:
+            outs = self._try("qkv", ins, L)
+            q, k, v = (m(xn) for m in projs) if outs is None else outs
+            # q/k-norm + RoPE + the KV-cache update, one launch
+            qr = ops.norm_rope_qkv(q, k, v, attn.q_norm.weight, attn.k_norm.weight,
+                                   c.num_attention_heads, c.num_key_value_heads, c.rms_norm_eps,
+                                   c.head_dim, c.rope_theta, cache.offset, cache.keys,
+                                   cache.values, cache.offset)
         o = ops.scaled_dot_product_attention(qr, cache.keys, cache.values, attn.scale,
                                              "causal" if L > 1 else None,
                                              kv_len=cache.offset + L,

@@ -59,8 +59,18 @@ def _close(got, want, tol=1e-2):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("L,offset", [(128, 0), (1, 128)])
-def test_qwen3_layer_config3(L, offset):
+def test_qwen3_layer_config3(L, offset, monkeypatch):
     from workloads import qwen3
+
+    fused = []  # the region model's fused q/k/v + prologue: taken (True) or declined
+    real = qwen3.ops.qkv_norm_rope
+
+    def counting(*a, **k):
+        out = real(*a, **k)
+        fused.append(out is not None)
+        return out
+
+    monkeypatch.setattr(qwen3.ops, "qkv_norm_rope", counting)
 
     cfg = qwen3.Qwen3Config()
     model = qwen3.build(cfg, seed=3, num_layers=1)
@@ -82,6 +92,8 @@ def test_qwen3_layer_config3(L, offset):
     torch.cuda.synchronize()
     assert torch.equal(y_orig, y_reg), "region splice changed the layer output bits"
     assert torch.equal(c_orig.keys, c_reg.keys) and torch.equal(c_orig.values, c_reg.values)
+    # prefill sizes take the fused launch, the decode step (M = 1) the two launches
+    assert fused == ([True] if not offset else [True, False]), fused
 
     W = export_layer(layer)
     kc = np.zeros((1, cfg.num_key_value_heads, 256, cfg.head_dim), np.float32)

@@ -74,3 +74,27 @@ def test_sized_regions_gate_try_sized(monkeypatch):
     assert w(torch.zeros(1), 3) == "original"
     assert W(torch.nn.Identity(), {})(torch.zeros(1), 3) == "original"  # no spec for the role
     assert calls == ["k1", "k1", "k1", "k1"]
+
+
+def test_sized_regions_serves_agrees_with_try():
+    """``_serves`` (a caller about to run a fused form of a cut) says yes
+    exactly where ``_try`` would launch: spec present, size served, fallback
+    predicate quiet."""
+    from autotuner_runtime import serve
+    from autotuner_runtime.kernels import KernelSpec
+
+    spec = KernelSpec(kernel_id="k2", name="mi_qmm_affine", input_names=("in0",),
+                      output_names=("out0",), source="mi_qmm_affine",
+                      output_shapes=(("in0.shape[0]",),), output_dtypes=("bfloat16",),
+                      fallback_predicate="in0.shape[0] > 4")
+
+    class W(serve.SizedRegions):
+        def forward(self, x, n):
+            return self._serves("role", [x], n)
+
+    w = W(torch.nn.Identity(), {"role": spec})
+    assert w(torch.zeros(3), 7) is True
+    assert w(torch.zeros(5), 7) is False                  # the predicate declines
+    w.set_ranges({"k2": [[1, 4]]})
+    assert w(torch.zeros(3), 7) is False and w(torch.zeros(3), 2) is True
+    assert W(torch.nn.Identity(), {})(torch.zeros(3), 2) is False  # no spec for the role

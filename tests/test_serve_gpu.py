@@ -76,6 +76,16 @@ def test_ranges_gate_the_kernels(monkeypatch):
     monkeypatch.setattr(kernels, "try_sized",
                         lambda spec, ins, init_value=None: launched.append(spec.kernel_id)
                         or real(spec, ins, init_value))
+    # a served q/k/v cut runs fused with the attention prologue (one launch)
+    fused = qwen3.ops.qkv_norm_rope
+
+    def counting_fused(*a, **k):
+        out = fused(*a, **k)
+        if out is not None:
+            launched.append("qwen3_qkv_proj")
+        return out
+
+    monkeypatch.setattr(qwen3.ops, "qkv_norm_rope", counting_fused)
     call = _make_call(cfg)
     for n, want in ((32, {"qwen3_gate_up_swiglu"}),
                     (100, {"qwen3_qkv_proj", "qwen3_gate_up_swiglu", "qwen3_down_add"})):
