@@ -1629,16 +1629,23 @@ int launch_mfma(const QParams &p, hipStream_t st) {
     const int64_t nt = ceil_div(p.Nout, 32);
     const bool large = p.M >= 512 || nt * ceil_div(p.M, 64) > 2048;
     if constexpr (P == 1) {
-        // (both widths; the grouped q/k/v epilogue binds one part per
-        // 32-feature tile. 8-bit took 32x128 tiles while its 64x128 tile
+        // (both widths. 8-bit took 32x128 tiles while its 64x128 tile
         // spilled; without the spill, LFM2's 8-bit out/down_proj at M = 2048
-        // went 84.9 -> 64.4 us on average)
-        constexpr int AL = EPI != EPI_GROUP3 ? 2 : 1;
+        // went 84.9 -> 64.4 us on average. The grouped q/k/v epilogue binds
+        // one part per tile, so it takes 64-feature tiles only when every
+        // part is a multiple of 64: LFM2's q/k/v at M = 2048, 6.35 -> 6.30 ms
+        // a prefill against 32-feature tiles)
+        const bool al2 = EPI != EPI_GROUP3 ||
+                         (p.pn[0] % 64 == 0 && p.pn[1] % 64 == 0 && p.pn[2] % 64 == 0);
         // wide single-part 4-bit outputs take 64x128 tiles from M = 128
         // (N = 9728: 23.1 -> 21.3 us; narrower N loses parallelism)
-        const bool wide = AL == 2 && p.M >= 128 && nt >= 256;
-        if ((large || wide) && mfma_lds_bytes<T, BITS, AL, 4>(p, wk) <= LDS_PER_CU)
-            return launch_mfma_cfg<T, BITS, AL, 4, EPI>(p, wk, st);
+        const bool wide = EPI != EPI_GROUP3 && p.M >= 128 && nt >= 256;
+        if ((large || wide) && al2 && mfma_lds_bytes<T, BITS, 2, 4>(p, wk) <= LDS_PER_CU)
+            return launch_mfma_cfg<T, BITS, 2, 4, EPI>(p, wk, st);
+        if constexpr (EPI == EPI_GROUP3) {
+            if (large && mfma_lds_bytes<T, BITS, 1, 4>(p, wk) <= LDS_PER_CU)
+                return launch_mfma_cfg<T, BITS, 1, 4, EPI>(p, wk, st);
+        }
     }
     if constexpr (P == 2) {
         if (large && mfma_lds_bytes<T, BITS, 2, 4>(p, wk) <= LDS_PER_CU)

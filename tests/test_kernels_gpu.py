@@ -508,6 +508,25 @@ def test_qmm_grouped3_mixed_tiles_qwen3_shape(M):
             _close(y[..., sl], want, "bfloat16")
 
 
+@pytest.mark.parametrize("Ns,bits", [((256, 64, 128), 4), ((256, 96, 64), 4), ((128, 64, 64), 8)])
+def test_qmm_grouped3_large_m_tiles(Ns, bits):
+    """From M = 512 the grouped launch takes 64-feature tiles when every part
+    is a multiple of 64, else 32-feature tiles: both bit for bit equal to the
+    three separate launches (which take their own tiles), and within the
+    oracle's tolerance on the first rows."""
+    r = rng(760 + sum(Ns) + bits)
+    M, K = 520, 512
+    x = oracle.round_to(r.normal(0, 1, (1, M, K)), "bfloat16")
+    qs = [_quant(761 + i, n, K, 64, bits) for i, n in enumerate(Ns)]
+    xd = to_torch(x, "bfloat16")
+    ws = [_dev(*q, "bfloat16") for q in qs]
+    got = ops.qmm_grouped3(xd, ws, 64, bits)
+    for q, w, y in zip(qs, ws, got):
+        assert torch.equal(y, ops.quantized_matmul(xd, *w, group_size=64, bits=bits))
+        want = oracle.quantized_matmul(x[:, :64], *q, 64, bits, "bfloat16")
+        _close(y[:, :64], want, "bfloat16")
+
+
 def test_qmm_grouped3_rejects_unaligned_parts():
     K = 256
     qs = [_quant(730 + i, n, K) for i, n in enumerate((64, 48, 64))]
