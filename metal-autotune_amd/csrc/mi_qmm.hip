@@ -767,6 +767,96 @@ __device__ __forceinline__ void head_norm_rope(const QParams &p, const Bound &bd
     }
 }
 
+// The same for 64-value heads (LFM2): four waves of two 32-feature tiles by
+// 128 tokens (C = 4), wave q holding features 32 a + 8 q + 4 h + e of tokens
+// m_blk + 32 c + r in acc[a][c][e]. norm_rope_kernel's form for D = 64 has
+// 8 lanes a row, lane t owning features 4t .. 4t+3 and partners 32 + 4t ..:
+// here lane t = 2q + h with a = 0 and its partners a = 1, and the butterfly
+// (4, 2, 1) pairs the token's eight chain sums, exchanged through xch
+// (8 x 128 floats of LDS). The angles are computed here: at the sizes this
+// form serves, other workgroups' loops cover the epilogue.
+template <typename T, int C>
+__device__ __forceinline__ void head_norm_rope64(const QParams &p, const Bound &bd,
+                                                 const f32x16 (&acc)[2][C], int q, int h, int r,
+                                                 int64_t m_blk, int64_t n_head, float *xch) {
+    constexpr int D = 64;
+    const int part = bd.gp;  // workgroup-uniform
+    const int64_t H = bd.Nout / D, hd = n_head / D;
+    const int64_t cap = part == 0 ? p.L : p.cap, pos0 = part == 0 ? 0 : p.pos0;
+    const int g0 = 8 * q + 4 * h;  // the lane's first feature; its partners g0 + 32
+    float v[C][2][4];
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[c][a][e] = (float)cvt<T>(acc[a][c][e]);
+    auto row_of = [&](int c) -> T * {
+        const int64_t m = m_blk + 32 * c + r;
+        const int64_t mm = m < p.M ? m : p.M - 1;
+        return (T *)bd.y0 + ((mm / p.L * H + hd) * cap + pos0 + mm % p.L) * D;
+    };
+    if (part == 2) {  // v: the cache rows as the GEMM rounds them
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            if (m_blk + 32 * c + r < p.M) {
+                T *orow = row_of(c);
+#pragma unroll
+                for (int a = 0; a < 2; ++a) st8(orow + 32 * a + g0, pack4<T>(v[c][a]));
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        float ss = 0.0f;  // the separate launch's lane t = 2q + h
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ss = __builtin_fmaf(v[c][a][e], v[c][a][e], ss);
+        xch[(2 * q + h) * (32 * C) + 32 * c + r] = ss;
+    }
+    __syncthreads();
+    const T *w = (const T *)p.nw[part];
+    float gw[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) unpack4<T>(ld8(w + 32 * a + g0), gw[a]);
+    float inv_freq[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        inv_freq[e] = exp2f(-(float)(2 * (g0 + e)) / (float)D * p.log2base);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int64_t m = m_blk + 32 * c + r;
+        float x[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) x[t] = xch[t * (32 * C) + 32 * c + r];
+        // level 4 pairs t with t ^ 4, level 2 with t ^ 2, level 1 with t ^ 1
+        const float sum = ((x[0] + x[4]) + (x[2] + x[6])) + ((x[1] + x[5]) + (x[3] + x[7]));
+        const float inv = 1.0f / __fsqrt_rn(sum / (float)D + p.eps);
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                v[c][a][e] = (float)cvt<T>(gw[a][e] * (float)cvt<T>(pin32<T>(v[c][a][e] * inv)));
+        const int64_t mm = m < p.M ? m : p.M - 1;
+        const float position = (float)(mm % p.L + p.offset) * p.rscale;
+        float r0[4], r1[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float sn, cs;
+            sincosf(position * inv_freq[e], &sn, &cs);
+            r0[e] = pin32<T>(rope_first(v[c][0][e], v[c][1][e], cs, sn));
+            r1[e] = pin32<T>(rope_second(v[c][0][e], v[c][1][e], cs, sn));
+        }
+        if (m < p.M) {
+            T *orow = row_of(c);
+            st8(orow + g0, pack4<T>(r0));
+            st8(orow + 32 + g0, pack4<T>(r1));
+        }
+    }
+}
+
 // One workgroup's tile: tokens [m_blk, m_blk + 32 * C) of the output features
 // starting at n_blk (32 * TN of them, per part). lds is the workgroup's static
 // LDS, at least MfmaShape::LDS bytes; the scale/bias tables live in the
@@ -883,7 +973,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
     // head_norm_rope), computed while the first stage's loads are in flight
     float hsn[4], hcs[4];
     auto head_angles = [&]() {
-        if constexpr (EPI == EPI_HEADNR) {
+        if constexpr (EPI == EPI_HEADNR && FH == 2) {
             const int64_t m = m_blk + r < p.M ? m_blk + r : p.M - 1;
             const float position = (float)(m % p.L + p.offset) * p.rscale;
 #pragma unroll
@@ -1201,8 +1291,11 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
                             }
                     }
                 }
-                if constexpr (EPI == EPI_HEADNR) {
-                    static_assert(FH == 2, "the whole-head tile runs eight waves");
+                if constexpr (EPI == EPI_HEADNR && FH == 1) {
+                    static_assert(A == 2 && C == 4, "64-value heads: two tiles by 128 tokens");
+                    head_norm_rope64<T, C>(p, bd, acc, kw, h, r, m_blk, n_wave, (float *)lds_dyn);
+                    return;
+                } else if constexpr (EPI == EPI_HEADNR) {
                     float hv[2][4];
 #pragma unroll
                     for (int a = 0; a < 2; ++a)
@@ -2046,6 +2139,31 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void q
                                                           (int64_t)blockIdx.y * 32);
 }
 
+// 64-value heads: two 32-feature tiles by 128 tokens a wave, four K-split
+// waves (the grouped q/k/v tile at M >= 512).
+template <typename T, int BITS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qmm_headnr64_kernel(
+    QParams p) {
+    __shared__ __attribute__((aligned(16))) char lds[MfmaShape<T, BITS, 2, 4, 4>::LDS];
+    qmm_mfma_tile<T, BITS, 2, 4, 4, EPI_HEADNR, KM_ONE>(p, lds, (int64_t)blockIdx.x * 64,
+                                                       (int64_t)blockIdx.y * 128);
+}
+
+template <typename T, int BITS>
+int launch_headnr64(QParams p, hipStream_t st) {
+    p.wk = 4;
+    if (!set_table(p, 4))
+        return fail(MI_ERR_UNSUPPORTED, "fused q/k/v: K = %lld too long for the scale/bias table",
+                    (long long)p.K);
+    // the four waves' scale/bias tables; the exchange (8 x 128 floats) reuses them
+    const int64_t dyn = 4 * 2 * 2 * (int64_t)sbt_layout(p.kslice, p.gs).array_bytes;
+    if (dyn < 8 * 128 * 4 || MfmaShape<T, BITS, 2, 4, 4>::LDS + dyn > LDS_PER_CU)
+        return fail(MI_ERR_UNSUPPORTED, "fused q/k/v tile LDS (K = %lld)", (long long)p.K);
+    const dim3 grid((unsigned)(p.Nout / 64), (unsigned)ceil_div(p.M, 128));
+    qmm_headnr64_kernel<T, BITS><<<grid, 256, (size_t)dyn, st>>>(p);
+    return launch_status("quantized q/k/v + norm + rope");
+}
+
 template <typename T, int BITS>
 int launch_headnr(QParams p, hipStream_t st) {
     p.wk = 4;
@@ -2086,15 +2204,16 @@ extern "C" int mi_qmm_affine_qkv_norm_rope(
         return fail(MI_ERR_ARG, "rows [%lld, %lld) exceed the cache capacity %lld",
                     (long long)kv_pos, (long long)(kv_pos + L), (long long)kv_cap);
     if (!(base > 0.0f)) return fail(MI_ERR_ARG, "rope base must be positive");
-    // The fused form covers 16-bit heads of 128 values rotated whole (not
-    // traditional), both norms, the MFMA path's shapes, and 16-byte aligned
-    // norm weights and outputs (the layout under which the separate launch
-    // takes the 16-lane form whose arithmetic the epilogue repeats).
-    // (4-bit weights: the 8-bit whole-head tile spills at three waves a SIMD)
-    if (dtype == MI_F32 || bits != 4 || D != 128 || rope_dims != 128 || traditional || !q_norm ||
-        !k_norm)
-        return fail(MI_ERR_UNSUPPORTED, "fused q/k/v + norm + rope covers 16-bit, 4-bit weights, "
-                                        "D = rope dims = 128, both norms");
+    // The fused form covers 16-bit heads of 128 values, or of 64 values from
+    // M = 512 (its 128-token tile; the grouped launch takes the same tile
+    // there), rotated whole (not traditional), both norms, the MFMA path's
+    // shapes, and 16-byte aligned norm weights and outputs (the layout under
+    // which the separate launch takes the 16- or 8-lane form whose arithmetic
+    // the epilogue repeats).
+    const bool d128 = D == 128 && rope_dims == 128, d64 = D == 64 && rope_dims == 64 && M >= 512;
+    if (dtype == MI_F32 || !(d128 || d64) || traditional || !q_norm || !k_norm)
+        return fail(MI_ERR_UNSUPPORTED, "fused q/k/v + norm + rope covers 16-bit, D = rope dims "
+                                        "= 128 (or 64 from M = 512), both norms");
     if (!mfma_shape_ok(M, K, N[0], group_size, bits) ||
         !mfma_shape_ok(M, K, N[1], group_size, bits))
         return fail(MI_ERR_UNSUPPORTED, "fused q/k/v + norm + rope: M=%lld K=%lld off the MFMA path",
@@ -2122,5 +2241,12 @@ extern "C" int mi_qmm_affine_qkv_norm_rope(
     p.log2base = (float)log2((double)base);
     p.rscale = scale;
     hipStream_t st = as_stream(stream);
-    return dtype == MI_BF16 ? launch_headnr<bf16, 4>(p, st) : launch_headnr<f16, 4>(p, st);
+    if (D == 64) {
+        if (dtype == MI_BF16)
+            return bits == 4 ? launch_headnr64<bf16, 4>(p, st) : launch_headnr64<bf16, 8>(p, st);
+        return bits == 4 ? launch_headnr64<f16, 4>(p, st) : launch_headnr64<f16, 8>(p, st);
+    }
+    if (dtype == MI_BF16)
+        return bits == 4 ? launch_headnr<bf16, 4>(p, st) : launch_headnr<bf16, 8>(p, st);
+    return bits == 4 ? launch_headnr<f16, 4>(p, st) : launch_headnr<f16, 8>(p, st);
 }

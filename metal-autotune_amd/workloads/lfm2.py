@@ -22,6 +22,9 @@ fall back to the original ops when a spec's predicate fires:
   [qmm(q), qmm(k), qmm(v)]              -> grouped3           (wrappers.py:156-164)
   q/k layernorm + rope + cache update   -> norm_rope_qkv      (wrappers.py:165-176)
 
+(the last two as one launch, ``ops.qkv_norm_rope``, where the qkv cut serves
+the call and the fused entry takes the shape: from 512 tokens)
+
 The reference's wrappers take the kernel path only for a fresh cache (conv
 state None, attention offset 0, wrappers.py:34,148); these kernels take the
 cache offset and conv state as inputs, so the region path also serves chunked
@@ -275,13 +278,23 @@ class Lfm2AttnRegions(SizedRegions):
         B, L, _ = x.shape
         xn = w.operator_norm(x)
         projs = (a.q_proj, a.k_proj, a.v_proj)
-        outs = self._try("qkv", [xn] + [t for m in projs for t in (m.weight, m.scales, m.biases)],
-                         L)
-        q, k, v = (m(xn) for m in projs) if outs is None else outs
-        qr = ops.norm_rope_qkv(q, k, v, a.q_layernorm.weight, a.k_layernorm.weight,
-                               c.num_attention_heads, c.num_key_value_heads, c.norm_eps,
-                               c.head_dim, c.rope_theta, cache.offset, cache.keys, cache.values,
-                               cache.offset)
+        ins = [xn] + [t for m in projs for t in (m.weight, m.scales, m.biases)]
+        qr = None
+        if self._serves("qkv", ins, L):
+            # the q/k/v cut with the prologue below in its epilogue, the same
+            # bits (None: shapes the fused entry does not take)
+            qr = ops.qkv_norm_rope(xn, [(m.weight, m.scales, m.biases) for m in projs],
+                                   a.q_layernorm.weight, a.k_layernorm.weight,
+                                   c.num_attention_heads, c.num_key_value_heads, c.norm_eps,
+                                   c.head_dim, c.rope_theta, cache.offset, cache.keys,
+                                   cache.values, cache.offset, c.group_size, c.bits)
+        if qr is None:
+            outs = self._try("qkv", ins, L)
+            q, k, v = (m(xn) for m in projs) if outs is None else outs
+            qr = ops.norm_rope_qkv(q, k, v, a.q_layernorm.weight, a.k_layernorm.weight,
+                                   c.num_attention_heads, c.num_key_value_heads, c.norm_eps,
+                                   c.head_dim, c.rope_theta, cache.offset, cache.keys,
+                                   cache.values, cache.offset)
         o = ops.scaled_dot_product_attention(qr, cache.keys, cache.values, a.scale,
                                              "causal" if L > 1 else None,
                                              kv_len=cache.offset + L,

@@ -5,8 +5,10 @@ Bar: bit for bit equal to the two entries it replaces (mi_qmm_affine_grouped3,
 then mi_norm_rope_qkv), whose own parity with the oracle the kernel tests hold;
 and within the bf16/fp16 region tolerance (1e-2 max-abs-normalised) of the
 oracle's quantized_matmul followed by its norm_rope. Shapes: the Qwen3 layer
-(32 q heads, 8 kv heads, D 128, K 2560) at the prefill sizes, ragged token
-counts, two sequences, a cache offset, and the shapes the fused entry declines.
+(32 q heads, 8 kv heads, D 128, K 2560) at the prefill sizes and the LFM2
+attention layer (D 64, K 2048) at 2048 tokens, 4- and 8-bit weights, ragged
+token counts, two sequences, a cache offset, and the shapes the fused entry
+declines.
 """
 
 from __future__ import annotations
@@ -41,36 +43,40 @@ def _caches(B, HK, cap, D, tdt):
     return kc, torch.full_like(kc, 6.0)
 
 
-@pytest.mark.parametrize("B,L,offset,K,dtype", [
-    (1, 128, 0, 2560, "bfloat16"),   # the Qwen3 prefill step
-    (1, 100, 0, 2560, "bfloat16"),   # ragged last token tile
-    (1, 9, 17, 512, "bfloat16"),     # smallest MFMA-path size, cache offset
-    (2, 40, 3, 512, "bfloat16"),     # two sequences: positions restart per sequence
-    (1, 300, 0, 512, "float16"),
+@pytest.mark.parametrize("B,L,offset,K,dtype,D,bits", [
+    (1, 128, 0, 2560, "bfloat16", 128, 4),   # the Qwen3 prefill step
+    (1, 100, 0, 2560, "bfloat16", 128, 4),   # ragged last token tile
+    (1, 9, 17, 512, "bfloat16", 128, 4),     # smallest MFMA-path size, cache offset
+    (2, 40, 3, 512, "bfloat16", 128, 4),     # two sequences: positions restart per sequence
+    (1, 300, 0, 512, "float16", 128, 4),
+    (1, 128, 5, 512, "bfloat16", 128, 8),
+    (1, 2048, 0, 2048, "bfloat16", 64, 4),   # the LFM2 prefill's attention layers
+    (1, 520, 40, 512, "bfloat16", 64, 8),    # ragged, cache offset
+    (2, 300, 0, 512, "float16", 64, 4),
 ])
-def test_qkv_norm_rope_equals_two_entries(B, L, offset, K, dtype):
-    H, HK, D, cap = 32, 8, 128, offset + L + 5
+def test_qkv_norm_rope_equals_two_entries(B, L, offset, K, dtype, D, bits):
+    H, HK, cap = 32, 8, offset + L + 5
     tdt = torch.bfloat16 if dtype == "bfloat16" else torch.float16
-    x, qs, qn, kn, ws = _case(1200 + L + B + offset, B, L, H, HK, D, K, dtype)
+    x, qs, qn, kn, ws = _case(1200 + L + B + offset + D + bits, B, L, H, HK, D, K, dtype, bits)
     xd, qw, kw = to_torch(x, dtype), to_torch(qn, dtype), to_torch(kn, dtype)
     kc, vc = _caches(B, HK, cap, D, tdt)
-    got = ops.qkv_norm_rope(xd, ws, qw, kw, H, HK, EPS, D, BASE, offset, kc, vc, offset)
+    got = ops.qkv_norm_rope(xd, ws, qw, kw, H, HK, EPS, D, BASE, offset, kc, vc, offset, 64, bits)
     assert got is not None, "the fused entry should cover this shape"
     kc2, vc2 = _caches(B, HK, cap, D, tdt)
-    q, k, v = ops.qmm_grouped3(xd, ws, 64, 4)
+    q, k, v = ops.qmm_grouped3(xd, ws, 64, bits)
     want = ops.norm_rope_qkv(q, k, v, qw, kw, H, HK, EPS, D, BASE, offset, kc2, vc2, offset)
     assert torch.equal(got, want)
     assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
     # rows outside [offset, offset + L) untouched
     assert bool((kc[:, :, :offset] == 5.0).all()) and bool((vc[:, :, offset + L:] == 6.0).all())
     # against the oracle (first sequence; q heads 0 and 31, the k cache rows)
-    x0 = x[:1]
-    yq = oracle.quantized_matmul(x0, *qs[0], 64, 4, dtype)
-    yk = oracle.quantized_matmul(x0, *qs[1], 64, 4, dtype)
+    x0 = x[:1, :128]
+    yq = oracle.quantized_matmul(x0, *qs[0], 64, bits, dtype)
+    yk = oracle.quantized_matmul(x0, *qs[1], 64, bits, dtype)
     wq = oracle.norm_rope(yq, qn, EPS, H, D, BASE, offset, dtype)
     wk = oracle.norm_rope(yk, kn, EPS, HK, D, BASE, offset, dtype)
-    for got_t, want_t in ((got[:1, [0, H - 1]], wq[:, [0, H - 1]]),
-                          (kc[:1, :, offset:offset + L], wk)):
+    for got_t, want_t in ((got[:1, [0, H - 1], :128], wq[:, [0, H - 1]]),
+                          (kc[:1, :, offset:offset + min(L, 128)], wk)):
         t = numeric.max_abs_normalised(got_t.cpu(), to_torch(want_t, dtype, "cpu"))
         assert t.passed, f"max-abs-normalised error {t.error:.3e} > {t.tol:.1e} ({t.detail})"
 
@@ -102,16 +108,16 @@ def test_qkv_norm_rope_replays_in_a_graph():
         assert torch.equal(out, want) and torch.equal(kc, kw_) and torch.equal(vc, vw_)
 
 
-@pytest.mark.parametrize("what", ["head64", "bits8", "fp32", "decode", "traditional", "no_norm"])
+@pytest.mark.parametrize("what", ["head64", "head96", "fp32", "decode", "traditional", "no_norm"])
 def test_qkv_norm_rope_declines_uncovered_shapes(what):
     """Shapes outside the fused form return None and launch nothing: the caller
     then runs grouped3 + norm_rope_qkv (the Qwen3 region model does)."""
     B, L, H, HK, D, K = 1, 16, 8, 2, 128, 256
     dtype, bits, trad = "bfloat16", 4, False
-    if what == "head64":
+    if what == "head64":  # 64-value heads below 512 tokens
         D = 64
-    elif what == "bits8":
-        bits = 8
+    elif what == "head96":
+        D = 96
     elif what == "fp32":
         dtype = "float32"
     elif what == "decode":
