@@ -18,10 +18,27 @@ int qmm_parts_launch(const void *x, const uint32_t *w, const void *s, const void
 
 namespace {
 
+// The sum over a wave, the same value in every lane: pairs within quads, then
+// quad sums across a half-row (mirror), half-row sums across a row (mirror),
+// all through DPP (no LDS round trip; the xor-shuffle tree took six
+// ds_bpermute instructions, each a dependent trip through the LDS unit), then
+// ((row 0 + row 1) + (row 2 + row 3)) from the four rows' lane 0. Every step
+// adds two values that every lane of the group holds alike, so all lanes end
+// with the same bits.
+template <int CTRL> __device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                 CTRL, 0xF, 0xF, false));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += dpp_f32<0xB1>(v);   // quad_perm [1, 0, 3, 2]: lane ^ 1
+    v += dpp_f32<0x4E>(v);   // quad_perm [2, 3, 0, 1]: lane ^ 2
+    v += dpp_f32<0x141>(v);  // row_half_mirror: lane 7 - i of each 8
+    v += dpp_f32<0x140>(v);  // row_mirror: lane 15 - i of each 16
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (r0 + r1) + (r2 + r3);
 }
 
 template <typename T>
