@@ -185,6 +185,24 @@ __device__ __forceinline__ float rope_second(float a, float c, float cs, float s
     return __builtin_fmaf(a, sn, c * cs);
 }
 
+// One DPP-moved copy of v (CTRL: the gfx9 DPP control; every lane active).
+template <int CTRL> __device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                 CTRL, 0xF, 0xF, false));
+}
+// The sum over each 16-lane row, the same bits in every lane of the row:
+// pairs within quads, then quad sums across a half-row and half-row sums
+// across the row (mirrors), each step adding two values the lanes of its
+// group hold alike. Four DPP adds, where an xor-shuffle tree takes four
+// dependent ds_bpermute trips through the LDS unit.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f32<0xB1>(v);   // quad_perm [1, 0, 3, 2]: lane ^ 1
+    v += dpp_f32<0x4E>(v);   // quad_perm [2, 3, 0, 1]: lane ^ 2
+    v += dpp_f32<0x141>(v);  // row_half_mirror: lane 7 - i of each 8
+    v += dpp_f32<0x140>(v);  // row_mirror: lane 15 - i of each 16
+    return v;
+}
+
 __host__ __device__ constexpr int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline int ilog2(int v) {

@@ -25,15 +25,8 @@ namespace {
 // ((row 0 + row 1) + (row 2 + row 3)) from the four rows' lane 0. Every step
 // adds two values that every lane of the group holds alike, so all lanes end
 // with the same bits.
-template <int CTRL> __device__ __forceinline__ float dpp_f32(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                                 CTRL, 0xF, 0xF, false));
-}
 __device__ __forceinline__ float wave_sum(float v) {
-    v += dpp_f32<0xB1>(v);   // quad_perm [1, 0, 3, 2]: lane ^ 1
-    v += dpp_f32<0x4E>(v);   // quad_perm [2, 3, 0, 1]: lane ^ 2
-    v += dpp_f32<0x141>(v);  // row_half_mirror: lane 7 - i of each 8
-    v += dpp_f32<0x140>(v);  // row_mirror: lane 15 - i of each 16
+    v = row16_sum(v);
     const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
     const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
     const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));

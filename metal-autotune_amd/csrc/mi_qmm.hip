@@ -317,12 +317,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QParams p) {
     for (int q = 0; q < P; ++q)
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-            float v = acc[q][m];
-            v += __shfl_xor(v, 8, 16);
-            v += __shfl_xor(v, 4, 16);
-            v += __shfl_xor(v, 2, 16);
-            v += __shfl_xor(v, 1, 16);
-            acc[q][m] = v;
+            acc[q][m] = row16_sum(acc[q][m]);  // the row's 16 lanes
         }
     if (j == 0 && n < bd.Nout) {
 #pragma unroll
@@ -531,12 +526,7 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
     for (int q = 0; q < P; ++q)
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-            float v = acc[q][m];
-            v += __shfl_xor(v, 8, 16);
-            v += __shfl_xor(v, 4, 16);
-            v += __shfl_xor(v, 2, 16);
-            v += __shfl_xor(v, 1, 16);
-            acc[q][m] = v;
+            acc[q][m] = row16_sum(acc[q][m]);  // the row's 16 lanes
         }
     if (j == 0 && n < bd.Nout) {
 #pragma unroll
