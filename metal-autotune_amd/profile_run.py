@@ -17,7 +17,9 @@ Runs, eagerly on the current stream:
 4. the two narrow projections of the layer with their residual epilogue
    (``ops.qmm_residual``, the [qmm, add] region): o_proj (x[128, 4096] @
    [2560, 4096]^T) and down_proj (x[128, 9728] @ [2560, 9728]^T), each over
-   enough weight copies to exceed the Infinity Cache.
+   enough weight copies to exceed the Infinity Cache;
+5. the fused q/k/v + q/k-norm + RoPE + cache write (``ops.qkv_norm_rope``,
+   32 q / 8 kv heads of 128 from x[128, 2560]) likewise.
 
 Prints one line per phase so the counter rows can be matched to phases by
 kernel name and launch order.
@@ -85,6 +87,22 @@ def main():
         torch.cuda.synchronize()
         print(f"phase {name}: {args.reps} x qmm+residual M={M} N={n_out} K={k_in}", flush=True)
         del wsn
+
+    # the q/k/v projections with q/k-norm, RoPE and the cache write in one
+    # launch (32 q / 8 kv heads of 128, K 2560), over enough weight copies
+    H, HK, D = 32, 8, 128
+    per = (H + 2 * HK) * D * K * 9 // 16
+    copies = (300 << 20) // per + 1
+    wq = [[random_quantized(n, K, gen, "cuda") for n in (H * D, HK * D, HK * D)]
+          for _ in range(copies)]
+    qn = torch.ones(D, dtype=torch.bfloat16, device="cuda")
+    kc = torch.zeros((1, HK, M, D), dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    for i in range(args.reps):
+        ops.qkv_norm_rope(x, wq[i % copies], qn, qn, H, HK, 1e-6, D, 1e6, 0, kc, vc, 0)
+    torch.cuda.synchronize()
+    print(f"phase qkv_norm_rope: {args.reps} x q/k/v + norm + rope M={M} heads {H}+{HK}+{HK} "
+          f"D={D} K={K}", flush=True)
 
 
 if __name__ == "__main__":
