@@ -20,7 +20,8 @@ Also measured live, with HIP events on the stream the kernels run on:
     stream floor: a read-only kernel over the same bytes and rotation;
   - lfm2_config5: the benchmark's config 5 beside the headline, the
     LFM2-1.2B-shaped hybrid prefilling 2048 tokens, 4- and 8-bit (ms per
-    prefill and tok/s, one HIP-graph replay each);
+    prefill and tok/s, one HIP-graph replay each), and at 4-bit its
+    regions-vs-op-stream ratio (the form of the reference's LFM2 headline);
   - cpu_baseline: the CPU oracle (the port; MLX is not installed) on a bounded
     sample -- one decoder layer at L=128 plus the lm_head for one token --
     scaled to the 36-layer model;
@@ -349,6 +350,30 @@ def lfm2_config5(torch, ops) -> dict:
                              "greedy_token": int(tok.item()),
                              "min_ms": round(c["min"], 3), "max_ms": round(c["max"], 3),
                              "se_ms": round(c["se"], 4), "samples": c["n"]}
+        if bits == 4:
+            # the reference's headline form for this model (its LFM2 artifact
+            # reports the patched against the untouched model): the same
+            # seeded model running its op stream, ABBA/BAAB pairs
+            base = lfm2.build(cfg, seed=0)
+            bcaches = base.make_cache(2048)
+
+            def base_step():
+                for bc in bcaches:
+                    bc.offset = 0
+                    if isinstance(bc, lfm2.ConvCache):
+                        bc.state = None
+                return ops.argmax(base(ids, bcaches).reshape(1, -1))
+
+            bg, btok = graph_of(base_step, torch)
+            r = measure.compare(bg.replay, g.replay)
+            out["4bit"]["regions_vs_ops"] = {
+                "model_ratio": round(r["median_ratio"], 4),
+                "ops_ms": round(r["median_base_ms"], 4),
+                "regions_ms": round(r["median_cand_ms"], 4),
+                "se_delta_ms": round(r["se_delta_ms"], 4), "stability": round(r["stability"], 3),
+                "observations": r["observations"],
+                "greedy_tokens_equal": int(btok.item()) == int(tok.item())}
+            del bg, base, bcaches
         del g, model, caches
         torch.cuda.empty_cache()
     return out
