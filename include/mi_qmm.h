@@ -207,8 +207,10 @@ int mi_norm_rope_qkv(const void *q, const void *k, const void *v, int64_t q_row_
  * k and v written into the caches [B, Hkv, kv_cap, D] at rows
  * [kv_pos, kv_pos + L). Every output equals mi_qmm_affine_grouped3 followed by
  * mi_norm_rope_qkv bit for bit; no intermediate q/k/v is written. Covers
- * bf16/fp16 x, 4- and 8-bit weights, D = rope_dims = 128 with B L > 8 or
- * D = rope_dims = 64 with B L >= 512, traditional = 0, both norms, K % 64 == 0
+ * bf16/fp16 x, 4- and 8-bit weights, D = rope_dims = 128 with 8 < B L <= 256
+ * or D = rope_dims = 64 with B L >= 512 (where the fused launch is the faster;
+ * the results are the same bits either way), traditional = 0, both norms,
+ * K % 64 == 0
  * and 16-byte aligned norm weights and outputs; other shapes return
  * MI_ERR_UNSUPPORTED (launch nothing), and the caller runs the two entries
  * instead. w, scales and biases are arrays of 3 in host memory. */

@@ -2194,16 +2194,20 @@ extern "C" int mi_qmm_affine_qkv_norm_rope(
         return fail(MI_ERR_ARG, "rows [%lld, %lld) exceed the cache capacity %lld",
                     (long long)kv_pos, (long long)(kv_pos + L), (long long)kv_cap);
     if (!(base > 0.0f)) return fail(MI_ERR_ARG, "rope base must be positive");
-    // The fused form covers 16-bit heads of 128 values, or of 64 values from
-    // M = 512 (its 128-token tile; the grouped launch takes the same tile
-    // there), rotated whole (not traditional), both norms, the MFMA path's
-    // shapes, and 16-byte aligned norm weights and outputs (the layout under
-    // which the separate launch takes the 16- or 8-lane form whose arithmetic
-    // the epilogue repeats).
-    const bool d128 = D == 128 && rope_dims == 128, d64 = D == 64 && rope_dims == 64 && M >= 512;
+    // The fused form covers 16-bit heads of 128 values up to M = 256 (past
+    // that the grouped launch's larger tiles win: at 384 tokens the fused
+    // launch took 34.9 against 33.7 us for the two launches, at 2048 134
+    // against 98; at 160 15.9 against 21.5), or of 64 values from M = 512
+    // (its 128-token tile; the grouped launch takes the same tile there),
+    // rotated whole (not traditional), both norms, the MFMA path's shapes, and
+    // 16-byte aligned norm weights and outputs (the layout under which the
+    // separate launch takes the 16- or 8-lane form whose arithmetic the
+    // epilogue repeats).
+    const bool d128 = D == 128 && rope_dims == 128 && M <= 256;
+    const bool d64 = D == 64 && rope_dims == 64 && M >= 512;
     if (dtype == MI_F32 || !(d128 || d64) || traditional || !q_norm || !k_norm)
         return fail(MI_ERR_UNSUPPORTED, "fused q/k/v + norm + rope covers 16-bit, D = rope dims "
-                                        "= 128 (or 64 from M = 512), both norms");
+                                        "= 128 up to M = 256 or 64 from M = 512, both norms");
     if (!mfma_shape_ok(M, K, N[0], group_size, bits) ||
         !mfma_shape_ok(M, K, N[1], group_size, bits))
         return fail(MI_ERR_UNSUPPORTED, "fused q/k/v + norm + rope: M=%lld K=%lld off the MFMA path",

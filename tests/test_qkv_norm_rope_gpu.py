@@ -48,7 +48,7 @@ def _caches(B, HK, cap, D, tdt):
     (1, 100, 0, 2560, "bfloat16", 128, 4),   # ragged last token tile
     (1, 9, 17, 512, "bfloat16", 128, 4),     # smallest MFMA-path size, cache offset
     (2, 40, 3, 512, "bfloat16", 128, 4),     # two sequences: positions restart per sequence
-    (1, 300, 0, 512, "float16", 128, 4),
+    (1, 256, 0, 512, "float16", 128, 4),     # the largest size the fused form takes at D 128
     (1, 128, 5, 512, "bfloat16", 128, 8),
     (1, 2048, 0, 2048, "bfloat16", 64, 4),   # the LFM2 prefill's attention layers
     (1, 520, 40, 512, "bfloat16", 64, 8),    # ragged, cache offset
@@ -108,7 +108,8 @@ def test_qkv_norm_rope_replays_in_a_graph():
         assert torch.equal(out, want) and torch.equal(kc, kw_) and torch.equal(vc, vw_)
 
 
-@pytest.mark.parametrize("what", ["head64", "head96", "fp32", "decode", "traditional", "no_norm"])
+@pytest.mark.parametrize("what", ["head64", "head96", "fp32", "decode", "long", "traditional",
+                                  "no_norm"])
 def test_qkv_norm_rope_declines_uncovered_shapes(what):
     """Shapes outside the fused form return None and launch nothing: the caller
     then runs grouped3 + norm_rope_qkv (the Qwen3 region model does)."""
@@ -122,6 +123,8 @@ def test_qkv_norm_rope_declines_uncovered_shapes(what):
         dtype = "float32"
     elif what == "decode":
         L = 4
+    elif what == "long":  # 128-value heads past 256 tokens: the two launches are faster
+        L = 264
     elif what == "traditional":
         trad = True
     x, _, qn, kn, ws = _case(1300, B, L, H, HK, D, K, dtype, bits)
