@@ -379,21 +379,34 @@ constexpr int QV_BATCH = 8;  // 16-byte weight chunks in flight per lane
 
 inline int64_t qmv_dot2_lds_bytes(int mr, int64_t K) { return mr * K * 2 + mr * (K / 32) * 4; }
 
-// PF: the x loads, then the first weight batch, are issued before x is
-// staged, so the weight stream runs under the staging and its two barriers
+// A workgroup of blockDim.x / 64 waves owns 4 output rows per wave (16 lanes a
+// row): 4 waves, or for single-output epilogues without PF up to 16 (WIDE),
+// sized by the host so the grid spreads the rows evenly over the CUs. Wider
+// workgroups are not used for the others: batches of two or three weight rows
+// take more than the 128 registers a lane may hold in a 16-wave workgroup,
+// and under PF the staging barriers wait for the x loads of every wave, which
+// queue behind the weight stream (one 10-wave workgroup per CU at N = 9728
+// waited 2.3 us for x against 1.5 us with 4 waves: 6.1 against 5.6 us a
+// launch).
+// PF (4 waves): the x loads, then the first weight batch, are issued before x
+// is staged, so the weight stream runs under the staging and its two barriers
 // (x first: vmcnt retires in issue order, so waiting for x then leaves the
 // weights in flight). Each thread holds at most two x chunks (MR * K / 8 <=
 // 512). It costs the batch registers through the staging, which pays when
 // the grid fits the chip in one round and not at N = 151936.
-template <typename T, int MR, int EPI, bool PF = false>
-__global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
+constexpr bool qmv_dot2_wide_ok(int epi) { return epi_parts(epi) == 1 && epi != EPI_GROUP3; }
+
+template <typename T, int MR, int EPI, bool PF = false, bool WIDE = false>
+__global__ __launch_bounds__(WIDE ? 1024 : 256) void qmv_dot2_kernel(QParams p) {
+    static_assert(!WIDE || (!PF && qmv_dot2_wide_ok(EPI)), "wide workgroups: single output, no PF");
     constexpr int P = epi_parts(EPI);
     typedef Magic<T> Mg;
     extern __shared__ uint4 xs_pairs[];  // [MR][K/8] pair blocks, then [MR][K/32] sums
     const int64_t K = p.K, words = K / 8, cpr = K / 32, G = K >> p.gs_log2;
     float *xsum = (float *)(xs_pairs + MR * words);
     const int lane = threadIdx.x & 63, j = lane & 15;
-    int64_t nb = (int64_t)blockIdx.x * 16;
+    const int bs = WIDE ? (int)blockDim.x : 256;  // threads
+    int64_t nb = (int64_t)blockIdx.x * (bs >> 4);
     const Bound bd = bind<EPI>(p, nb);
     const int64_t n = nb + (threadIdx.x >> 6) * 4 + (lane >> 4);
     const int64_t nrow = n < bd.Nout ? n : bd.Nout - 1;
@@ -436,12 +449,12 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
                           __builtin_amdgcn_perm(d.w, d.y, 0x05040100u),
                           __builtin_amdgcn_perm(d.w, d.y, 0x07060302u));
     };
+    const int nw = (int)words;  // 32-bit index math: MR * K < 2^31
     if constexpr (PF) {
-        // every thread issues both loads (a clamped, valid chunk when past the
-        // end) so the issue order, and with it the waits, is the same in all
-        // waves: x, then the weights
+        // 256 threads (4 waves). Every thread issues both loads (a clamped,
+        // valid chunk when past the end) so the issue order, and with it the
+        // waits, is the same in all waves: x, then the weights
         uint4 d[2];
-        const int nw = (int)words;  // <= 512 here: 32-bit index math
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             int idx = (int)threadIdx.x + 256 * t;
@@ -457,15 +470,14 @@ __global__ __launch_bounds__(256) void qmv_dot2_kernel(QParams p) {
             if (idx < MR * words) xs_pairs[idx] = pairs(d[t]);
         }
     } else {
-        const int nw = (int)words;  // 32-bit index math: MR * K < 2^31
-        for (int idx = threadIdx.x; idx < MR * nw; idx += 256) {
+        for (int idx = threadIdx.x; idx < MR * nw; idx += bs) {
             const int m = MR == 1 ? 0 : idx / nw, w = idx - m * nw;
             xs_pairs[idx] = pairs(ld16(x + (int64_t)(m < mr ? m : mr - 1) * K + 8 * w));
         }
     }
     __syncthreads();
     const int ncpr = (int)cpr;
-    for (int idx = threadIdx.x; idx < MR * ncpr; idx += 256) {
+    for (int idx = threadIdx.x; idx < MR * ncpr; idx += bs) {
         const int m = MR == 1 ? 0 : idx / ncpr, c = idx - m * ncpr;
         float s = 0.0f;
 #pragma unroll
@@ -1779,19 +1791,42 @@ int launch_mfma(const QParams &p, hipStream_t st) {
 
 template <typename T, int EPI>
 int launch_qmv_dot2(const QParams &p, int mr, hipStream_t st) {
-    const dim3 grid((unsigned)ceil_div(p.Nout, 16), (unsigned)ceil_div(p.M, mr));
+    // weights requested under the x staging when the 4-wave grid is at most
+    // four workgroups per CU (measured: N = 9728 gains, N = 151936 loses)
+    const int64_t gy = ceil_div(p.M, mr);
+    const bool pf = mr == 1 && ceil_div(p.Nout, 16) * gy <= 1024 && p.K / 8 <= 512;
+    // Waves per workgroup (4 rows each) without PF: as many as spread the
+    // rows evenly over the CUs in one round of workgroups (N = 9728: 10 waves,
+    // 244 workgroups, at most 40 rows a CU, where 16-row workgroups put 48 on
+    // some CUs and 32 on the others: M = 2 7.5 -> 7.2 us, M = 4 11.0 -> 9.6);
+    // 4 when the rows take more than one round of 16-wave workgroups, for the
+    // grouped q/k/v epilogue, whose workgroups each lie inside one part, and
+    // for the several-output ones.
+    int waves = 4;
+    if constexpr (qmv_dot2_wide_ok(EPI)) {
+        const int64_t wv = ceil_div(p.Nout, 4 * (int64_t)device_cus());
+        if (!pf && wv <= 16) waves = wv < 4 ? 4 : (int)wv;
+    }
+    const int bs = 64 * waves;
+    const dim3 grid((unsigned)ceil_div(p.Nout, 4 * waves), (unsigned)gy);
     const size_t lds = (size_t)qmv_dot2_lds_bytes(mr, p.K);
-    // weights requested under the x staging when the grid is at most four
-    // workgroups per CU (measured: N = 9728 gains, N = 151936 loses)
-    const bool pf = (int64_t)grid.x * grid.y <= 1024 && p.K / 8 <= 512;
-    if (mr == 1 && pf)
-        qmv_dot2_kernel<T, 1, EPI, true><<<grid, 256, lds, st>>>(p);
-    else if (mr == 1)
-        qmv_dot2_kernel<T, 1, EPI><<<grid, 256, lds, st>>>(p);
-    else if (mr == 2)
-        qmv_dot2_kernel<T, 2, EPI><<<grid, 256, lds, st>>>(p);
-    else
-        qmv_dot2_kernel<T, 4, EPI><<<grid, 256, lds, st>>>(p);
+    if (pf) {
+        qmv_dot2_kernel<T, 1, EPI, true><<<grid, bs, lds, st>>>(p);
+    } else if (waves == 4) {
+        if (mr == 1)
+            qmv_dot2_kernel<T, 1, EPI><<<grid, bs, lds, st>>>(p);
+        else if (mr == 2)
+            qmv_dot2_kernel<T, 2, EPI><<<grid, bs, lds, st>>>(p);
+        else
+            qmv_dot2_kernel<T, 4, EPI><<<grid, bs, lds, st>>>(p);
+    } else if constexpr (qmv_dot2_wide_ok(EPI)) {
+        if (mr == 1)
+            qmv_dot2_kernel<T, 1, EPI, false, true><<<grid, bs, lds, st>>>(p);
+        else if (mr == 2)
+            qmv_dot2_kernel<T, 2, EPI, false, true><<<grid, bs, lds, st>>>(p);
+        else
+            qmv_dot2_kernel<T, 4, EPI, false, true><<<grid, bs, lds, st>>>(p);
+    }
     return launch_status("quantized matmul (dot2 qmv)");
 }
 

@@ -129,6 +129,36 @@ def test_qmm_config2_shape(M):
     _close(y, want, "bfloat16")
 
 
+@pytest.mark.parametrize("M,N", [(2, 9728), (3, 9728), (4, 9004), (1, 9004)])
+@pytest.mark.parametrize("resid", [False, True])
+def test_qmv_wide_workgroups_equal_four_wave_ones(M, N, resid):
+    """The decode GEMV sizes its workgroups from N and the CU count (up to 16
+    waves, so the rows spread evenly over the CUs). A row's arithmetic does
+    not depend on the workgroup: the first 2048 rows of the wide launch equal,
+    bit for bit, a launch over those rows alone (4 waves). N = 9004 leaves a
+    partial last workgroup; M = 3 leaves a token of the 4-token blocks empty;
+    M = 1 at K = 5120 runs without the early weight prefetch. Both against
+    qmm_factored at the bf16 bar."""
+    r = rng(260 + M + N)
+    K = 5120 if M == 1 else 2560
+    x = oracle.round_to(r.normal(0, 1, (M, K)), "bfloat16")
+    wq, s, b = _quant(17, N, K)
+    res = oracle.round_to(r.normal(0, 1, (M, N)), "bfloat16")
+    dev = _dev(wq, s, b, "bfloat16")
+    xd, rd = to_torch(x, "bfloat16"), to_torch(res, "bfloat16")
+    head = [t[:2048].contiguous() for t in dev]
+    if resid:
+        wide = ops.qmm_residual(xd, *dev, rd)
+        narrow = ops.qmm_residual(xd, *head, rd[:, :2048].contiguous())
+    else:
+        wide = ops.quantized_matmul(xd, *dev)
+        narrow = ops.quantized_matmul(xd, *head)
+    assert torch.equal(wide[:, :2048], narrow)
+    t = oracle.qmm_factored(x, wq, s, b, 64, 4, "bfloat16")
+    want = oracle.round_to(res.astype(np.float64) + t, "bfloat16") if resid else t
+    _close(wide, want, "bfloat16")
+
+
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
 @pytest.mark.parametrize("bits,gs", [(4, 64), (8, 64), (4, 32), (4, 128), (8, 32)])
 @pytest.mark.parametrize("M", [1, 7, 40, 130, 520])
