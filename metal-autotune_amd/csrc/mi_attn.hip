@@ -24,10 +24,12 @@
 //                           registers for the whole kernel;
 //   lane (q = lane%32, half) then holds 16 of the 32 keys of its query row, so
 //   the row max/sum needs one xor-32 shuffle;
-//   O^T[d][q] += V^T . P^T  A = V^T from a transposed LDS tile, B = P^T
-//                           straight from the S^T registers (bf16/fp16): the
-//                           k order inside each MFMA is permuted to match the
-//                           S^T register layout, for both operands.
+//   O^T[d][q] += V^T . P^T  A = V^T, read by transposing LDS loads from the
+//                           V tile staged key-major as it sits in memory,
+//                           B = P^T straight from the S^T registers
+//                           (bf16/fp16): the k order inside each MFMA is
+//                           permuted to match the S^T register layout, for
+//                           both operands.
 // Online softmax in the log2 domain, fp32 running max/sum, one division at
 // the end. Causal masking is bottom-right aligned (query i sees keys
 // j <= i + Lk - Lq) and key tiles past the last visible key are skipped.
@@ -54,8 +56,10 @@ template <> struct AMfma<f16> {
 };
 
 constexpr int ATT_KT = 32;       // keys per tile
-constexpr int ATT_VP = ATT_KT + 8;  // padded V^T-tile row (elements)
 constexpr int ATT_STREAMS = 4;   // key-tile streams per query row
+// Row pitch (elements) of a key-major V tile in LDS: D + 16, so the four key
+// rows one 16-lane group reads (32 bytes of each) start 8 banks apart.
+template <int D> constexpr int att_vpitch() { return D + 16; }
 
 // Online-softmax state of one wave: O^T tiles (lane = query column r, half
 // h2), the row's reference maximum m (log2 units) and this lane's half of the
@@ -77,8 +81,9 @@ template <int D> __device__ __forceinline__ void attn_init(AttnState<D> &st) {
 // One key tile kt, in two steps. attn_scores: s = S^T (s[i]: key
 // kt*32 + 8*(i/4) + 4*h2 + i%4 of query row qrow) -> masking and the lazily
 // rescaled online softmax; p gets the tile's probabilities. attn_pv:
-// O^T += V^T . P^T, vts = the tile's V^T in LDS (D rows of ATT_VP). attn_tile
-// runs both; the split kernel runs the scores before its V tile is written.
+// O^T += V^T . P^T, vs = the tile's V in LDS (32 key rows of att_vpitch<D>()
+// elements). attn_tile runs both; the split kernel runs the scores before its
+// V tile is written.
 template <int D>
 __device__ __forceinline__ void attn_scores(AttnState<D> &st, const f32x16 &s, float (&p)[16],
                                             int kt, int64_t q0, int64_t qrow, int64_t off,
@@ -124,13 +129,32 @@ __device__ __forceinline__ void attn_scores(AttnState<D> &st, const f32x16 &s, f
     st.l += psum;
 }
 
+// Four 16-bit values by ds_read_b64_tr_b16. Within each 16-lane group, with
+// lane s addressing four consecutive values E[s][0..3], lane 4a + b receives
+// (E[a][b], E[a + 4][b], E[a + 8][b], E[a + 12][b]) (probed on gfx950: LDS
+// filled with each value's index, lanes addressing rows of 4 and of 16).
+template <typename T>
+__device__ __forceinline__ typename Vec<T>::x4 lds_read_tr4(const T *p) {
+    typedef short S4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) S4 *LP;
+    return __builtin_bit_cast(typename Vec<T>::x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((LP)p));
+}
+
+// A fragment of O^T += V^T . P^T for lane (r, h2), MFMA k2 of head-dim tile
+// t: V^T[32 t + r][keys 16 k2 + 4 h2 + (0..3), then the same + 8]. Lane s of
+// 16-lane group G addresses key row 16 k2 + 4 h2 + s / 4 (h2 = G / 2) at
+// column 32 t + 16 (G % 2) + 4 (s % 4); by the rule above lane 4a + b of the
+// group (r = 16 (G % 2) + 4a + b) then receives column 32 t + r of the key
+// rows 16 k2 + 4 h2 + 0..3.
 template <typename T, int D>
-__device__ __forceinline__ void attn_pv(AttnState<D> &st, const float (&p)[16], const T *vts,
-                                        int h2, int r) {
+__device__ __forceinline__ void attn_pv(AttnState<D> &st, const float (&p)[16], const T *vs,
+                                        int lane) {
 #pragma clang fp contract(off)
-    constexpr int DT = D / 32;
+    constexpr int DT = D / 32, VP = att_vpitch<D>();
     typedef typename Vec<T>::x8 V8;
     typedef typename Vec<T>::x4 V4;
+    const int s = lane & 15, g = lane >> 4;
+    const T *vl = vs + (4 * (g >> 1) + (s >> 2)) * VP + 16 * (g & 1) + 4 * (s & 3);
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
         V8 pb;
@@ -138,9 +162,9 @@ __device__ __forceinline__ void attn_pv(AttnState<D> &st, const float (&p)[16], 
         for (int e = 0; e < 8; ++e) pb[e] = (T)p[8 * k2 + e];
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
-            const T *vr = vts + (32 * t + r) * ATT_VP + 16 * k2 + 4 * h2;
-            const V4 lo = __builtin_bit_cast(V4, *(const uint2 *)vr);
-            const V4 hi = __builtin_bit_cast(V4, *(const uint2 *)(vr + 8));
+            const T *vr = vl + 16 * k2 * VP + 32 * t;
+            const V4 lo = lds_read_tr4<T>(vr);
+            const V4 hi = lds_read_tr4<T>(vr + 8 * VP);
             V8 a;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -153,12 +177,12 @@ __device__ __forceinline__ void attn_pv(AttnState<D> &st, const float (&p)[16], 
 }
 
 template <typename T, int D>
-__device__ __forceinline__ void attn_tile(AttnState<D> &st, const f32x16 &s, const T *vts, int kt,
+__device__ __forceinline__ void attn_tile(AttnState<D> &st, const f32x16 &s, const T *vs, int kt,
                                           int64_t q0, int64_t qrow, int64_t off, int64_t Lk,
-                                          int causal, float scale_log2, int h2, int r) {
+                                          int causal, float scale_log2, int h2, int lane) {
     float p[16];
     attn_scores<D>(st, s, p, kt, q0, qrow, off, Lk, causal, scale_log2, h2);
-    attn_pv<T, D>(st, p, vts, h2, r);
+    attn_pv<T, D>(st, p, vs, lane);
 }
 
 // Folding a later stream's state (mw, lw, o_w) into a running (m, l, o):
@@ -227,7 +251,7 @@ __device__ __forceinline__ int attn_ntiles(int64_t q0, int64_t off, int64_t Lk, 
 
 template <int D> struct SplitLds {
     static constexpr int DT = D / 32;
-    static constexpr int VT_BYTES = D * ATT_VP * 2;            // one wave's V^T tile
+    static constexpr int VT_BYTES = ATT_KT * att_vpitch<D>() * 2;  // one wave's V tile
     static constexpr int PART_FLOATS = DT * 16 * 64 + 2 * 64;  // one wave's state
     static constexpr int BYTES = ATT_STREAMS * VT_BYTES > ATT_STREAMS * PART_FLOATS * 4
                                      ? ATT_STREAMS * VT_BYTES
@@ -281,11 +305,11 @@ __global__ __launch_bounds__(64 * ATT_STREAMS) void attn_split_kernel(
     const int ntiles = attn_ntiles(q0, off, Lk, causal);
     const T *kb = k + (b * HK + hk) * cap * D;
     const T *vb = v + (b * HK + hk) * cap * D;
-    T *vts = (T *)(lds + wave * L::VT_BYTES);  // this wave's V^T tile
+    T *vs = (T *)(lds + wave * L::VT_BYTES);  // this wave's V tile (key-major)
 
     // A tile's loads: the K rows as MFMA A fragments (key r, head-dim chunk
     // 16 s + 8 h2), and V as 16-byte chunks (key r, chunk h2 + 2 i) for the
-    // transposed LDS tile. Keys past Lk read the last key (in bounds): their
+    // key-major LDS tile. Keys past Lk read the last key (in bounds): their
     // scores are masked and their V rows zeroed.
     constexpr int VCH = D / 16;  // V chunks per lane
     uint4 kf[DS], vreg[VCH];
@@ -321,21 +345,18 @@ __global__ __launch_bounds__(64 * ATT_STREAMS) void attn_split_kernel(
             s = AMfma<T>::mma(__builtin_bit_cast(V8, kf[ks]), __builtin_bit_cast(V8, qf[ks]), s);
         float p[16];
         attn_scores<D>(st, s, p, kt, q0, qrow, off, Lk, causal, scale_log2, h2);
-        // V^T tile: this wave's own LDS, written and read by this wave only
+        // V tile: this wave's own LDS, written and read by this wave only
         // (its LDS instructions execute in order)
         const bool vok = (int64_t)kt * ATT_KT + r < Lk;
 #pragma unroll
-        for (int i = 0; i < VCH; ++i) {
-            const V8 vv = __builtin_bit_cast(V8, vok ? vreg[i] : make_uint4(0, 0, 0, 0));
-            const int dc = h2 + 2 * i;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) vts[(dc * 8 + e) * ATT_VP + r] = vv[e];
-        }
+        for (int i = 0; i < VCH; ++i)
+            *(uint4 *)(vs + r * att_vpitch<D>() + (h2 + 2 * i) * 8) =
+                vok ? vreg[i] : make_uint4(0, 0, 0, 0);
         if (kt + ATT_STREAMS < ntiles) fetch(kt + ATT_STREAMS);  // under this tile's math
-        attn_pv<T, D>(st, p, vts, h2, r);
+        attn_pv<T, D>(st, p, vs, lane);
     }
 
-    // Merge: every wave leaves its stream's (o, l, m) in LDS (over the V^T
+    // Merge: every wave leaves its stream's (o, l, m) in LDS (over the V
     // tiles) as 16-byte words; wave w then folds the four streams, in stream
     // order, for O^T tile t = w (D = 64: tiles 0 and 1) and stores that tile.
     // Each wave recomputes the same (m, l) chain, so the result is that of one
@@ -344,7 +365,7 @@ __global__ __launch_bounds__(64 * ATT_STREAMS) void attn_split_kernel(
     // 4j .. 4j + 3 of tile t at t * 4 + j), then float2 (l, m) [64].
     float4 *part = (float4 *)lds;
     constexpr int PART4 = L::PART_FLOATS / 4;  // one wave's state in float4
-    __syncthreads();  // every wave is done with its V^T tile
+    __syncthreads();  // every wave is done with its V tile
     {
         float4 *pp = part + (size_t)wave * PART4;
 #pragma unroll
@@ -405,7 +426,7 @@ __global__ __launch_bounds__(256) void attn_shared_kernel(
     constexpr int DS = D / 16;
     typedef typename Vec<T>::x8 V8;
     __shared__ __attribute__((aligned(16))) T ks[ATT_KT * KP];
-    __shared__ __attribute__((aligned(16))) T vts[D * ATT_VP];
+    __shared__ __attribute__((aligned(16))) T vs[ATT_KT * att_vpitch<D>()];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int h2 = lane >> 5, r = lane & 31;
@@ -449,8 +470,7 @@ __global__ __launch_bounds__(256) void attn_shared_kernel(
 
     // K/V tile staging: each thread owns CH 16-byte chunks of a tile; the
     // chunks of the next tile are loaded into registers while this one
-    // computes. Consecutive lanes take consecutive keys, so the transposed V
-    // stores of a wave hit consecutive 2-byte LDS addresses.
+    // computes. Both tiles are key-major in LDS (V is read transposed).
     constexpr int CH = ATT_KT * D / 8 / 256;
     uint4 kreg[CH], vreg[CH];
     auto fetch = [&](int kt) {
@@ -488,9 +508,7 @@ __global__ __launch_bounds__(256) void attn_shared_kernel(
                 const int key = c % ATT_KT, dc = c / ATT_KT;
                 const bool ok = (int64_t)kt * ATT_KT + key < Lk;
                 *(uint4 *)(ks + key * KP + dc * 8) = ok ? kreg[i] : make_uint4(0, 0, 0, 0);
-                const V8 vv = __builtin_bit_cast(V8, ok ? vreg[i] : make_uint4(0, 0, 0, 0));
-#pragma unroll
-                for (int e = 0; e < 8; ++e) vts[(dc * 8 + e) * ATT_VP + key] = vv[e];
+                *(uint4 *)(vs + key * att_vpitch<D>() + dc * 8) = ok ? vreg[i] : make_uint4(0, 0, 0, 0);
             }
             const int nk = next_tile(kt);  // the next tile in stream order
             if (nk >= 0) fetch(nk);
@@ -505,7 +523,7 @@ __global__ __launch_bounds__(256) void attn_shared_kernel(
                         __builtin_bit_cast(V8, *(const uint4 *)(ks + r * KP + 16 * kq + 8 * h2));
                     s = AMfma<T>::mma(a, __builtin_bit_cast(V8, qf[kq]), s);
                 }
-                attn_tile<T, D>(cur, s, vts, kt, q0, qrow, off, Lk, causal, scale_log2, h2, r);
+                attn_tile<T, D>(cur, s, vs, kt, q0, qrow, off, Lk, causal, scale_log2, h2, lane);
             }
         }
         if (active) {
