@@ -65,7 +65,8 @@ struct QParams {
     int sbninst;               // qmm_mfma_kernel: DMA instructions per scale/bias table array
     unsigned sbmagic;          // ceil(2^20 / (sbp / 2)): v / (sbp / 2) as (v * sbmagic) >> 20
     int ks;                    // K parts (kpart_count): each is split over the wk waves
-    int kslice;                // k values of the longest wave chunk (ks * wk chunks of K)
+    int kslice;                // k values a scale/bias table covers (a wave chunk, or all of K)
+    int kint;                  // interleaved K split (kint_of): wave w takes stages w, w + wk, ...
     float *part;               // non-null: write K part blockIdx.z's sums, fp32 [ks, M, Nout]
     // EPI_HEADNR (the parts are q, k, v; py[] = q_out [B, Hq, L, D], k_cache,
     // v_cache [B, Hkv, cap, D]; D = 128)
@@ -875,7 +876,8 @@ __device__ __forceinline__ void head_norm_rope64(const QParams &p, const Bound &
 // loop and its running sums compile away).
 enum KMode { KM_ONE = 0, KM_LOOP = 1, KM_PART = 2 };
 
-template <typename T, int BITS, int A, int C, int WK, int EPI, int KM = KM_ONE, int FH = 1>
+template <typename T, int BITS, int A, int C, int WK, int EPI, int KM = KM_ONE, int FH = 1,
+          bool KI = false>
 __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64_t n_blk,
                                               int64_t m_blk, int kz = 0) {
     // The body uses gfx950 buffer resources, which the host target cannot
@@ -937,8 +939,10 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
     const int pitch = p.sbp;
     const SbtLayout tl = {pitch, p.sbninst, p.sbninst * 256};  // sbt_layout(p.kslice, p.gs)
     extern __shared__ __attribute__((aligned(16))) char lds_dyn[];
-    const char *sbt = lds_dyn + wv * (A * 2 * tl.array_bytes);
-    float *psum = (float *)(lds_dyn + FH * wk * (A * 2 * tl.array_bytes));  // sums over K parts
+    // one scale/bias table per wave, or one for the workgroup (kint)
+    static_assert(!KI || (KM == KM_ONE && FH == 1), "interleaved K split: one K part, four waves");
+    const char *sbt = lds_dyn + (KI ? 0 : wv) * (A * 2 * tl.array_bytes);
+    float *psum = (float *)(lds_dyn + (KI ? 1 : FH * wk) * (A * 2 * tl.array_bytes));  // sums over K parts
     typedef __attribute__((address_space(3))) void *lds_ptr;
     // x DMA: instruction i writes stage rows 8i..8i+7; lane l fills row
     // 8i + l/8 at swizzled position l%8, i.e. it loads chunk (l%8) ^ swz(row).
@@ -989,15 +993,24 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
         }
     };
     for (int kp = 0; kp < nparts; ++kp) {  // workgroup-uniform
+        // The wave's stages: kbeg + st * kstep for st < nst. Contiguous
+        // chunks: chunk cix of the ks * wk chunks of K. Interleaved (KI, one
+        // K part, WK waves): stages kw, kw + WK, ...; a wave past the last
+        // stage (K < WK * XK) runs none, and its prologue loads read the last
+        // stage.
         const int cix = (KM == KM_PART ? kz : kp) * wk + kw;
         const int sbeg = (cix * nstages) >> cshift;
-        const int kbeg = sbeg * XK;
-        const int nst = (((cix + 1) * nstages) >> cshift) - sbeg;
+        const int kbeg = KI ? (kw < nstages ? kw : nstages - 1) * XK : sbeg * XK;
+        const int nst = KI ? (kw < nstages ? (nstages - kw + WK - 1) / WK : 0)
+                           : (((cix + 1) * nstages) >> cshift) - sbeg;
+        constexpr int kstep = KI ? WK * XK : XK;
         // Scale/bias table (layout in sbt_layout): dword v of an array holds
         // groups gbase + 2j, +1 of tile row v / (pitch / 2), j = v % (pitch / 2).
         // Issued before the ring prologue, so the first stage's wait covers it.
-        const int gbase = (kbeg >> gshift) & ~1;
-        for (int i = 0; i < tl.ninst; ++i) {
+        // kint: one table from group 0, its DMA instructions dealt to the
+        // waves in turn (a barrier after the wait below).
+        const int gbase = KI ? 0 : (kbeg >> gshift) & ~1;
+        for (int i = KI ? kw : 0; i < tl.ninst; i += KI ? WK : 1) {
             int v = 64 * i + lane;
             v = v < 16 * pitch ? v : 16 * pitch - 1;
             const int rr = (int)(((unsigned)v * p.sbmagic) >> 20), j = v - rr * (pitch >> 1);
@@ -1016,7 +1029,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
         const int hg = (p.gs <= VPC) ? h * (VPC >> gshift) : 0;
         const int sbrow = (r * pitch + hg - gbase) * 2;
         auto issue = [&](int st, char *slot) {
-            const int k0 = kbeg + st * XK;
+            const int k0 = kbeg + st * kstep;
             const uint32_t xs = (uint32_t)k0 * sizeof(T);
             if constexpr (XREMAT) {
                 // opaque per stage, so the offsets are not hoisted out of the loop
@@ -1057,7 +1070,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
         auto load_w = [&](int st, uint4 (&wd)[A][SPS]) {
 #pragma unroll
             for (int u = 0; u < SPS; ++u) {
-                const int ku = kbeg + st * XK + u * SS;
+                const int ku = kbeg + st * kstep + u * SS;
                 const uint32_t ws = (uint32_t)(ku / VPW) * 4;
 #pragma unroll
                 for (int a = 0; a < A; ++a) {
@@ -1102,7 +1115,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
             for (int a = 0; a < A; ++a)
 #pragma unroll
                 for (int u = 0; u < SPS; ++u) {
-                    const char *sb = tb + 2 * a * tab + sbrow + ((kbeg + st * XK + u * SS) >> gshift) * 2;
+                    const char *sb = tb + 2 * a * tab + sbrow + ((kbeg + st * kstep + u * SS) >> gshift) * 2;
                     sq[a][u] = *(const uint16_t *)sb;
                     bq[a][u] = *(const uint16_t *)(sb + tab);
                 }
@@ -1112,6 +1125,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
         head_angles();
         // the table's DMAs were issued before the prologue's
         wait_vmcnt<Sh::TABLE_VMCNT>();
+        if constexpr (KI) __syncthreads();  // every wave's share of the table has landed
         load_sb(0);
         for (int st0 = 0; st0 < nst; st0 += Sh::UNROLL) {
 #pragma unroll
@@ -1471,14 +1485,14 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
-template <typename T, int BITS, int A, int C, int WK, int EPI, int KM>
+template <typename T, int BITS, int A, int C, int WK, int EPI, int KM, bool KI = false>
 __global__ __launch_bounds__(64 * WK)
 __attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<A, C>()))) void qmm_mfma_kernel(
     QParams p) {
     constexpr int TN = (epi_parts(EPI) == 1) ? A : 1;
     __shared__ __attribute__((aligned(16))) char lds[MfmaShape<T, BITS, A, C, WK>::LDS];
-    qmm_mfma_tile<T, BITS, A, C, WK, EPI, KM>(p, lds, (int64_t)blockIdx.x * (32 * TN),
-                                              (int64_t)blockIdx.y * (32 * C), (int)blockIdx.z);
+    qmm_mfma_tile<T, BITS, A, C, WK, EPI, KM, 1, KI>(p, lds, (int64_t)blockIdx.x * (32 * TN),
+                                                     (int64_t)blockIdx.y * (32 * C), (int)blockIdx.z);
 }
 
 // Block i of a run of n feature tiles that take g workgroups each (the g
@@ -1602,6 +1616,25 @@ inline int kslice_of(int64_t K, int ks, int wk) {
     return (int)ceil_div(K / XK, (int64_t)ks * wk) * XK;
 }
 
+// The interleaved K split: from M = 512 (a function of M and K only, so every
+// tile shape at one (M, K) adds in the same order), one K part, four waves,
+// while one scale/bias table over all of K fits the index multiplier of
+// set_table (K / gs up to 358). The four waves then read adjacent stages
+// (the 32-byte pieces of one 128-byte line of each weight row) at a time:
+// LFM2's 2048-token prefill 6.30 -> 6.15 ms; at M = 128 the contiguous
+// chunks keep more lines in flight per row and were the faster.
+constexpr int64_t KINT_MIN_M = 512;
+inline bool kint_of(const QParams &p, int wk) {
+    if (p.M < KINT_MIN_M || p.ks != 1 || wk != 4) return false;
+    const SbtLayout tl = sbt_layout(p.K, p.gs);
+    return 8ll * tl.pitch * tl.pitch < (1ll << 20);
+}
+// k values one scale/bias table covers, and the tables of a workgroup
+inline int table_kslice(const QParams &p, int wk) {
+    return kint_of(p, wk) ? (int)p.K : kslice_of(p.K, p.ks, wk);
+}
+inline int table_count(const QParams &p, int wk) { return kint_of(p, wk) ? 1 : wk; }
+
 // Running sums over the K parts (a workgroup that runs them in turn): one
 // fp32 per accumulator register and lane.
 inline int64_t mfma_sum_bytes(const QParams &p, int A, int C) {
@@ -1613,9 +1646,9 @@ inline int64_t mfma_sum_bytes(const QParams &p, int A, int C) {
 // (a table too long for the index multiplier of set_table counts as not
 // fitting, so the dispatcher takes another kernel)
 inline int64_t mfma_dyn_bytes(const QParams &p, int A, int C, int wk) {
-    const SbtLayout tl = sbt_layout(kslice_of(p.K, p.ks, wk), p.gs);
+    const SbtLayout tl = sbt_layout(table_kslice(p, wk), p.gs);
     if (8ll * tl.pitch * tl.pitch >= (1ll << 20)) return 1ll << 40;
-    return (int64_t)wk * A * 2 * tl.array_bytes + mfma_sum_bytes(p, A, C);
+    return (int64_t)table_count(p, wk) * A * 2 * tl.array_bytes + mfma_sum_bytes(p, A, C);
 }
 
 // LDS of one workgroup: the static stage slots plus the dynamic part.
@@ -1629,7 +1662,8 @@ int64_t mfma_lds_bytes(const QParams &p, int wk) {
 // pitch / 2 (exact for indices below 16 pitch while 8 pitch^2 < 2^20, i.e.
 // K slices up to 360 groups; the host refuses longer ones).
 inline bool set_table(QParams &p, int wk) {
-    p.kslice = kslice_of(p.K, p.ks, wk);
+    p.kint = kint_of(p, wk) ? 1 : 0;
+    p.kslice = table_kslice(p, wk);
     const SbtLayout tl = sbt_layout(p.kslice, p.gs);
     p.sbp = tl.pitch;
     p.sbninst = tl.ninst;
@@ -1651,6 +1685,12 @@ int launch_mfma_cfg(QParams p, int wk, hipStream_t st) {
                     (long long)p.K);
     const dim3 grid((unsigned)ceil_div(p.Nout, 32 * TN), (unsigned)ceil_div(p.M, 32 * C),
                     p.part ? (unsigned)p.ks : 1u);
+    if constexpr (KM == KM_ONE) {
+        if (p.kint) {
+            qmm_mfma_kernel<T, BITS, A, C, 4, EPI, KM, true><<<grid, 64 * wk, dyn, st>>>(p);
+            return launch_status("quantized matmul (mfma)");
+        }
+    }
     qmm_mfma_kernel<T, BITS, A, C, 4, EPI, KM><<<grid, 64 * wk, dyn, st>>>(p);
     return launch_status("quantized matmul (mfma)");
 }
@@ -2170,19 +2210,23 @@ template <typename T, int BITS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void qmm_headnr64_kernel(
     QParams p) {
     __shared__ __attribute__((aligned(16))) char lds[MfmaShape<T, BITS, 2, 4, 4>::LDS];
-    qmm_mfma_tile<T, BITS, 2, 4, 4, EPI_HEADNR, KM_ONE>(p, lds, (int64_t)blockIdx.x * 64,
+    qmm_mfma_tile<T, BITS, 2, 4, 4, EPI_HEADNR, KM_ONE, 1, true>(p, lds, (int64_t)blockIdx.x * 64,
                                                        (int64_t)blockIdx.y * 128);
 }
 
 template <typename T, int BITS>
 int launch_headnr64(QParams p, hipStream_t st) {
     p.wk = 4;
-    if (!set_table(p, 4))
+    // (the grouped q/k/v launch it stands for takes the interleaved split at
+    // these sizes too; where that does not apply, it declines)
+    if (!set_table(p, 4) || !p.kint)
         return fail(MI_ERR_UNSUPPORTED, "fused q/k/v: K = %lld too long for the scale/bias table",
                     (long long)p.K);
-    // the four waves' scale/bias tables; the exchange (8 x 128 floats) reuses them
-    const int64_t dyn = 4 * 2 * 2 * (int64_t)sbt_layout(p.kslice, p.gs).array_bytes;
-    if (dyn < 8 * 128 * 4 || MfmaShape<T, BITS, 2, 4, 4>::LDS + dyn > LDS_PER_CU)
+    // the scale/bias tables (one, shared, under the interleaved K split this
+    // tile always runs at: M >= 512); the exchange (8 x 128 floats) reuses them
+    int64_t dyn = table_count(p, 4) * 2 * 2 * (int64_t)sbt_layout(p.kslice, p.gs).array_bytes;
+    dyn = dyn > 8 * 128 * 4 ? dyn : 8 * 128 * 4;
+    if (MfmaShape<T, BITS, 2, 4, 4>::LDS + dyn > LDS_PER_CU)
         return fail(MI_ERR_UNSUPPORTED, "fused q/k/v tile LDS (K = %lld)", (long long)p.K);
     const dim3 grid((unsigned)(p.Nout / 64), (unsigned)ceil_div(p.M, 128));
     qmm_headnr64_kernel<T, BITS><<<grid, 256, (size_t)dyn, st>>>(p);

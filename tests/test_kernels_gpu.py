@@ -377,7 +377,7 @@ def test_qmm_split_gate(M):
     _close(bx, bx_want, "bfloat16")
 
 
-@pytest.mark.parametrize("M", [1, 20, 128, 300])
+@pytest.mark.parametrize("M", [1, 20, 128, 300, 600])
 def test_qmm_dual_and_swiglu(M):
     r = rng(700 + M)
     K, N = 1024, 384
@@ -394,6 +394,34 @@ def test_qmm_dual_and_swiglu(M):
     _close(sw, oracle.swiglu(gw, uw, "bfloat16"), "bfloat16")
     # fused epilogue == swiglu of the unfused outputs, bit for bit
     assert torch.equal(sw, ops.swiglu(g, u))
+    # either output equals the single-weight launch, bit for bit
+    assert torch.equal(g, ops.quantized_matmul(xd, *_dev(*q1, "bfloat16")))
+    assert torch.equal(u, ops.quantized_matmul(xd, *_dev(*q3, "bfloat16")))
+
+
+@pytest.mark.parametrize("K", [128, 256, 640, 2048])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_qmm_interleaved_k_split(K, bits):
+    """From M = 512 the four K-split waves take interleaved stages (wave w:
+    stages w, w + 4, ...) with one scale/bias table for the workgroup; at
+    K = 128 two waves have no stage of their own, at K = 640 the waves take
+    3, 3, 2 and 2 stages. Within tolerance of the
+    oracle, with the residual epilogue, and row-independent: the last rows
+    of an M = 520 launch equal, bit for bit, the same rows leading an
+    M = 600 launch (other tiles, the same order)."""
+    M, N = 520, 256
+    r = rng(1400 + K + bits)
+    x = oracle.round_to(r.normal(0, 1, (1, M, K)), "bfloat16")
+    res = oracle.round_to(r.normal(0, 1, (1, M, N)), "bfloat16")
+    q = _quant(1401 + K, N, K, bits=bits)
+    xd, rd, w = to_torch(x, "bfloat16"), to_torch(res, "bfloat16"), _dev(*q, "bfloat16")
+    y = ops.quantized_matmul(xd, *w, bits=bits)
+    t = oracle.quantized_matmul(x, *q, 64, bits, "bfloat16")
+    _close(y, t, "bfloat16")
+    yr = ops.qmm_residual(xd, *w, rd, bits=bits)
+    _close(yr, oracle.round_to(res.astype(np.float64) + t, "bfloat16"), "bfloat16")
+    ext = torch.cat([xd[:, 500:], xd[:, :580]], dim=1).contiguous()  # M = 600
+    assert torch.equal(y[:, 500:], ops.quantized_matmul(ext, *w, bits=bits)[:, :20])
 
 
 @pytest.mark.parametrize("M,N", [(128, 9728), (100, 9728), (128, 8704), (128, 5120)])
@@ -468,9 +496,10 @@ def test_qmm_dual_8bit_large_tiles(dtype):
     """The 8-bit dual from M = 512 runs 128-token tiles whose x offsets are
     rebuilt per stage (M = 520: a last tile of 8 tokens, whose other 120 rows
     read zeros past the end of x). Within tolerance of the oracle; rows
-    [0, 512) and [480, 520) equal, bit for bit, MFMA launches of M = 512 and
-    M = 40 (32-token tiles, the same K split; M <= 8 would take the GEMV,
-    whose factored sums round differently); every element written (NaN-filled
+    [0, 512) equal, bit for bit, a launch of M = 512, and the ragged rows
+    [480, 520) the first 40 rows of a launch of M = 552 that starts with
+    them (whole tiles there; every M from 512 adds K in the same interleaved
+    order, smaller M in contiguous chunks); every element written (NaN-filled
     output); the fused SwiGLU equals swiglu of the unfused pair bit for bit."""
     M, N, K = 520, 512, 1024
     r = rng(790)
@@ -484,9 +513,11 @@ def test_qmm_dual_8bit_large_tiles(dtype):
     uw = oracle.quantized_matmul(x, *q3, 64, 8, dtype)
     _close(g, gw, dtype)
     _close(u, uw, dtype)
-    for lo, hi in ((0, 512), (480, 520)):
-        pg, pu = ops.qmm_dual(xd[:, lo:hi].contiguous(), *w, bits=8)
-        assert torch.equal(g[:, lo:hi], pg) and torch.equal(u[:, lo:hi], pu), (lo, hi)
+    pg, pu = ops.qmm_dual(xd[:, :512].contiguous(), *w, bits=8)
+    assert torch.equal(g[:, :512], pg) and torch.equal(u[:, :512], pu)
+    ext = torch.cat([xd[:, 480:520], xd[:, :512]], dim=1).contiguous()  # M = 552
+    pg, pu = ops.qmm_dual(ext, *w, bits=8)
+    assert torch.equal(g[:, 480:520], pg[:, :40]) and torch.equal(u[:, 480:520], pu[:, :40])
     sw = ops.qmm_dual(xd, *w, bits=8, swiglu=True)
     assert torch.equal(sw, ops.swiglu(g, u))
     _close(sw, oracle.swiglu(gw, uw, dtype), dtype)
@@ -495,7 +526,7 @@ def test_qmm_dual_8bit_large_tiles(dtype):
     assert torch.equal(poisoned, sw)
 
 
-@pytest.mark.parametrize("M", [1, 3, 8, 16, 40, 128, 300])
+@pytest.mark.parametrize("M", [1, 3, 8, 16, 40, 128, 300, 520])
 @pytest.mark.parametrize("bits,dtype", [(4, "bfloat16"), (8, "float16"), (4, "float32")])
 def test_qmm_grouped3_equals_three_launches(M, bits, dtype):
     """q/k/v in one launch: bit-identical to three mi_qmm_affine calls (the
