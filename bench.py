@@ -18,6 +18,9 @@ Also measured live, with HIP events on the stream the kernels run on:
     (HBM GB/s vs 8 TB/s) and M=128 (TFLOP/s vs the MFMA peak), rotating more
     weight copies than the 256 MB Infinity Cache holds; beside M=1, the
     stream floor: a read-only kernel over the same bytes and rotation;
+  - decode: config 4's greedy decode step after the prefill (one token through
+    the 36 layers and the lm_head, every projection a GEMV at M = 1), ms per
+    token and its weight + K/V bytes against the HBM peak;
   - lfm2_config5: the benchmark's config 5 beside the headline, the
     LFM2-1.2B-shaped hybrid prefilling 2048 tokens, 4- and 8-bit (ms per
     prefill and tok/s, one HIP-graph replay each), and at 4-bit its
@@ -257,6 +260,49 @@ def regions_vs_ops(torch, ops, qwen3, ids) -> dict:
                         "one call of this library), not MLX's kernels (MLX is not installed)"}
 
 
+def decode_step(model, ids, token, torch, ops, peaks=None) -> dict:
+    """One greedy decode step of the config 4 model after its 128-token prefill:
+    the prefill's greedy token at position 128 through the 36 layers (every
+    projection a GEMV at M = 1, attention over 129 keys) and the tied lm_head,
+    then the argmax; captured once into a HIP graph, every replay rewriting
+    cache row 128. Timed the reference's way (median of 9 samples of >= 20 ms).
+    Decode reads every weight once: the model's weight bytes (quantized
+    weights, scales, biases, norms; the tied embedding once, as the lm_head)
+    plus the K/V rows read, over the step time, against the HBM peak."""
+    import measure
+
+    caches = model.make_cache(PROMPT + 1)
+    for c in caches:
+        c.offset = 0
+    model(ids, caches)  # the prefill fills cache rows 0 .. 127
+    torch.cuda.synchronize()
+    nxt = torch.tensor([[token]], device="cuda", dtype=ids.dtype)
+
+    def step():
+        for c in caches:
+            c.offset = PROMPT
+        return ops.argmax(model(nxt, caches).reshape(1, -1))
+
+    g, tok = graph_of(step, torch)
+    c = measure.clock(g.replay)
+    ms = c["median"]
+    wbytes = sum(b.numel() * b.element_size() for _, b in model.named_buffers())
+    kv = sum(2 * c_.keys[..., : PROMPT + 1, :].numel() * c_.keys.element_size() for c_ in caches)
+    byts = wbytes + kv
+    gbs = byts / ms / 1e6
+    out = {"ms_per_token": round(ms, 4), "tok_s": round(1000.0 / ms, 1),
+           "clock": {"median_ms": round(ms, 4), "min_ms": round(c["min"], 4),
+                     "max_ms": round(c["max"], 4), "se_ms": round(c["se"], 5), "samples": c["n"],
+                     "replays_per_sample": c["calls_per_sample"]},
+           "bytes": int(byts), "weight_bytes": int(wbytes), "kv_bytes": int(kv),
+           "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+           "greedy_token": int(tok.item())}
+    if peaks:
+        out["hbm_frac_measured_peak"] = round(gbs / peaks["hbm"]["read_GB_s"], 4)
+    del g, caches
+    return out
+
+
 def cpu_baseline(model, ids, torch):
     """Oracle on the host cores: one layer at L=128 + lm_head for one token,
     scaled to 36 layers."""
@@ -435,6 +481,7 @@ def main():
 
     roof = dominant_kernel(model, torch, ops, peaks)
     qmm = qmm_config2(torch, ops, peaks)
+    decode = decode_step(model, ids, token, torch, ops, peaks)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(model, ids, torch)
@@ -465,6 +512,7 @@ def main():
         "peaks": peaks_line,
         "regions_vs_ops": rvo,
         "qmm": qmm,
+        "decode": decode,
         "lfm2_config5": hybrid,
         "cpu_baseline": cpu,
     }
