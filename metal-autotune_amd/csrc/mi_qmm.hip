@@ -397,19 +397,25 @@ inline int64_t qmv_dot2_lds_bytes(int mr, int64_t K) { return mr * K * 2 + mr * 
 // the grid fits the chip in one round and not at N = 151936.
 constexpr bool qmv_dot2_wide_ok(int epi) { return epi_parts(epi) == 1 && epi != EPI_GROUP3; }
 
-template <typename T, int MR, int EPI, bool PF = false, bool WIDE = false>
+// LPR: lanes per output row, 16 (4 rows a wave) or 64 (a row a wave, for long
+// K: a K = 9728 row is 19 chunks a lane at 16 lanes, loaded in three batches
+// one after another, and about 5 at 64, one batch).
+template <typename T, int MR, int EPI, bool PF = false, bool WIDE = false, int LPR = 16>
 __global__ __launch_bounds__(WIDE ? 1024 : 256) void qmv_dot2_kernel(QParams p) {
     static_assert(!WIDE || (!PF && qmv_dot2_wide_ok(EPI)), "wide workgroups: single output, no PF");
+    static_assert(LPR == 16 || (LPR == 64 && !PF && qmv_dot2_wide_ok(EPI)),
+                  "a row a wave: single output, no PF");
+    constexpr int RPW = 64 / LPR;  // rows a wave
     constexpr int P = epi_parts(EPI);
     typedef Magic<T> Mg;
     extern __shared__ uint4 xs_pairs[];  // [MR][K/8] pair blocks, then [MR][K/32] sums
     const int64_t K = p.K, words = K / 8, cpr = K / 32, G = K >> p.gs_log2;
     float *xsum = (float *)(xs_pairs + MR * words);
-    const int lane = threadIdx.x & 63, j = lane & 15;
+    const int lane = threadIdx.x & 63, j = lane & (LPR - 1);
     const int bs = WIDE ? (int)blockDim.x : 256;  // threads
-    int64_t nb = (int64_t)blockIdx.x * (bs >> 4);
+    int64_t nb = (int64_t)blockIdx.x * ((bs >> 6) * RPW);
     const Bound bd = bind<EPI>(p, nb);
-    const int64_t n = nb + (threadIdx.x >> 6) * 4 + (lane >> 4);
+    const int64_t n = nb + (threadIdx.x >> 6) * RPW + lane / LPR;
     const int64_t nrow = n < bd.Nout ? n : bd.Nout - 1;
     const int64_t m0 = (int64_t)blockIdx.y * MR;
     const int mr = (int)((p.M - m0) < MR ? (p.M - m0) : MR);
@@ -430,7 +436,7 @@ __global__ __launch_bounds__(WIDE ? 1024 : 256) void qmv_dot2_kernel(QParams p) 
     auto load_batch = [&](int64_t base) {
 #pragma unroll
         for (int i = 0; i < QV_BATCH; ++i) {
-            const int64_t c = base + 16 * i;
+            const int64_t c = base + LPR * i;
             const int64_t cc = c < cpr ? c : cpr - 1;
             const int64_t g = (cc * 32) >> p.gs_log2;
 #pragma unroll
@@ -499,14 +505,14 @@ __global__ __launch_bounds__(WIDE ? 1024 : 256) void qmv_dot2_kernel(QParams p) 
 #pragma unroll
         for (int m = 0; m < MR; ++m) acc[q][m] = 0.0f;
 
-    for (int64_t base = j; base < cpr; base += 16 * QV_BATCH) {
+    for (int64_t base = j; base < cpr; base += LPR * QV_BATCH) {
         // (Without PF the compiler sinks each chunk's loads to its use behind
         // the `c >= cpr` exit, so a lane fetches its chunks one after another;
         // at 58 registers eight waves per SIMD keep the loads in flight.)
         if (!PF || base != j) load_batch(base);
 #pragma unroll
         for (int i = 0; i < QV_BATCH; ++i) {
-            const int64_t c = base + 16 * i;
+            const int64_t c = base + LPR * i;
             if (c >= cpr) break;
 #pragma unroll
             for (int q = 0; q < P; ++q) {
@@ -540,6 +546,14 @@ __global__ __launch_bounds__(WIDE ? 1024 : 256) void qmv_dot2_kernel(QParams p) 
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             acc[q][m] = row16_sum(acc[q][m]);  // the row's 16 lanes
+            if constexpr (LPR == 64) {  // then the wave's four 16-lane sums
+                const int v = __builtin_bit_cast(int, acc[q][m]);
+                const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(v, 0));
+                const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(v, 16));
+                const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(v, 32));
+                const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(v, 48));
+                acc[q][m] = (r0 + r1) + (r2 + r3);
+            }
         }
     if (j == 0 && n < bd.Nout) {
 #pragma unroll
@@ -1835,37 +1849,58 @@ int launch_qmv_dot2(const QParams &p, int mr, hipStream_t st) {
     // four workgroups per CU (measured: N = 9728 gains, N = 151936 loses)
     const int64_t gy = ceil_div(p.M, mr);
     const bool pf = mr == 1 && ceil_div(p.Nout, 16) * gy <= 1024 && p.K / 8 <= 512;
-    // Waves per workgroup (4 rows each) without PF: as many as spread the
-    // rows evenly over the CUs in one round of workgroups (N = 9728: 10 waves,
-    // 244 workgroups, at most 40 rows a CU, where 16-row workgroups put 48 on
-    // some CUs and 32 on the others: M = 2 7.5 -> 7.2 us, M = 4 11.0 -> 9.6);
-    // 4 when the rows take more than one round of 16-wave workgroups, for the
-    // grouped q/k/v epilogue, whose workgroups each lie inside one part, and
-    // for the several-output ones.
+    // A row a wave (LPR 64) for single-output launches over long rows (K >
+    // 4096, more than 8 chunks a lane at 16 lanes a row). Waves per workgroup
+    // without PF: as many as spread the rows evenly over the CUs in one round
+    // of workgroups (N = 9728 at 4 rows a wave: 10 waves, 244 workgroups, at
+    // most 40 rows a CU, where 16-row workgroups put 48 on some CUs and 32 on
+    // the others: M = 2 7.5 -> 7.2 us, M = 4 11.0 -> 9.6); 4 when the rows
+    // take more than one round of 16-wave workgroups, for the grouped q/k/v
+    // epilogue, whose workgroups each lie inside one part, and for the
+    // several-output ones.
+    constexpr bool wide_ok = qmv_dot2_wide_ok(EPI);
+    const bool row_wave = wide_ok && !pf && p.K / 32 > 128;
+    const int rpw = row_wave ? 1 : 4;
     int waves = 4;
-    if constexpr (qmv_dot2_wide_ok(EPI)) {
-        const int64_t wv = ceil_div(p.Nout, 4 * (int64_t)device_cus());
+    if constexpr (wide_ok) {
+        const int64_t wv = ceil_div(p.Nout, rpw * (int64_t)device_cus());
         if (!pf && wv <= 16) waves = wv < 4 ? 4 : (int)wv;
     }
     const int bs = 64 * waves;
-    const dim3 grid((unsigned)ceil_div(p.Nout, 4 * waves), (unsigned)gy);
+    const dim3 grid((unsigned)ceil_div(p.Nout, rpw * waves), (unsigned)gy);
     const size_t lds = (size_t)qmv_dot2_lds_bytes(mr, p.K);
     if (pf) {
         qmv_dot2_kernel<T, 1, EPI, true><<<grid, bs, lds, st>>>(p);
-    } else if (waves == 4) {
+    } else if (!row_wave && waves == 4) {
         if (mr == 1)
             qmv_dot2_kernel<T, 1, EPI><<<grid, bs, lds, st>>>(p);
         else if (mr == 2)
             qmv_dot2_kernel<T, 2, EPI><<<grid, bs, lds, st>>>(p);
         else
             qmv_dot2_kernel<T, 4, EPI><<<grid, bs, lds, st>>>(p);
-    } else if constexpr (qmv_dot2_wide_ok(EPI)) {
-        if (mr == 1)
-            qmv_dot2_kernel<T, 1, EPI, false, true><<<grid, bs, lds, st>>>(p);
-        else if (mr == 2)
-            qmv_dot2_kernel<T, 2, EPI, false, true><<<grid, bs, lds, st>>>(p);
-        else
-            qmv_dot2_kernel<T, 4, EPI, false, true><<<grid, bs, lds, st>>>(p);
+    } else if constexpr (wide_ok) {
+        if (row_wave && waves == 4) {
+            if (mr == 1)
+                qmv_dot2_kernel<T, 1, EPI, false, false, 64><<<grid, bs, lds, st>>>(p);
+            else if (mr == 2)
+                qmv_dot2_kernel<T, 2, EPI, false, false, 64><<<grid, bs, lds, st>>>(p);
+            else
+                qmv_dot2_kernel<T, 4, EPI, false, false, 64><<<grid, bs, lds, st>>>(p);
+        } else if (row_wave) {
+            if (mr == 1)
+                qmv_dot2_kernel<T, 1, EPI, false, true, 64><<<grid, bs, lds, st>>>(p);
+            else if (mr == 2)
+                qmv_dot2_kernel<T, 2, EPI, false, true, 64><<<grid, bs, lds, st>>>(p);
+            else
+                qmv_dot2_kernel<T, 4, EPI, false, true, 64><<<grid, bs, lds, st>>>(p);
+        } else {
+            if (mr == 1)
+                qmv_dot2_kernel<T, 1, EPI, false, true><<<grid, bs, lds, st>>>(p);
+            else if (mr == 2)
+                qmv_dot2_kernel<T, 2, EPI, false, true><<<grid, bs, lds, st>>>(p);
+            else
+                qmv_dot2_kernel<T, 4, EPI, false, true><<<grid, bs, lds, st>>>(p);
+        }
     }
     return launch_status("quantized matmul (dot2 qmv)");
 }

@@ -137,8 +137,8 @@ def test_qmv_wide_workgroups_equal_four_wave_ones(M, N, resid):
     not depend on the workgroup: the first 2048 rows of the wide launch equal,
     bit for bit, a launch over those rows alone (4 waves). N = 9004 leaves a
     partial last workgroup; M = 3 leaves a token of the 4-token blocks empty;
-    M = 1 at K = 5120 runs without the early weight prefetch. Both against
-    qmm_factored at the bf16 bar."""
+    M = 1 at K = 5120 runs without the early weight prefetch, a row a wave.
+    Both against qmm_factored at the bf16 bar."""
     r = rng(260 + M + N)
     K = 5120 if M == 1 else 2560
     x = oracle.round_to(r.normal(0, 1, (M, K)), "bfloat16")
@@ -157,6 +157,25 @@ def test_qmv_wide_workgroups_equal_four_wave_ones(M, N, resid):
     t = oracle.qmm_factored(x, wq, s, b, 64, 4, "bfloat16")
     want = oracle.round_to(res.astype(np.float64) + t, "bfloat16") if resid else t
     _close(wide, want, "bfloat16")
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 2560, 9728), (2, 2048, 8192), (4, 600, 9728), (1, 8, 4160)])
+def test_qmv_row_per_wave_long_k(M, N, K):
+    """Past K = 4096 the single-output decode GEMV gives each row a whole wave
+    (64 lanes; about 5 chunks a lane at K = 9728, the Qwen3 down_proj at
+    decode) and adds its four 16-lane sums in a fixed order. Within the bf16
+    bar of qmm_factored, with and without the residual; N = 8 is a grid of
+    fewer rows than one workgroup holds."""
+    r = rng(1500 + M + N + K)
+    x = oracle.round_to(r.normal(0, 1, (M, K)), "bfloat16")
+    res = oracle.round_to(r.normal(0, 1, (M, N)), "bfloat16")
+    wq, s, b = _quant(1501, N, K)
+    dev = _dev(wq, s, b, "bfloat16")
+    xd, rd = to_torch(x, "bfloat16"), to_torch(res, "bfloat16")
+    t = oracle.qmm_factored(x, wq, s, b, 64, 4, "bfloat16")
+    _close(ops.quantized_matmul(xd, *dev), t, "bfloat16")
+    _close(ops.qmm_residual(xd, *dev, rd), oracle.round_to(res.astype(np.float64) + t, "bfloat16"),
+           "bfloat16")
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
