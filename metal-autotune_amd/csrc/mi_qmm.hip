@@ -1846,9 +1846,13 @@ int launch_mfma(const QParams &p, hipStream_t st) {
 template <typename T, int EPI>
 int launch_qmv_dot2(const QParams &p, int mr, hipStream_t st) {
     // weights requested under the x staging when the 4-wave grid is at most
-    // four workgroups per CU (measured: N = 9728 gains, N = 151936 loses)
+    // four workgroups per CU (measured: N = 9728 gains, N = 151936 loses),
+    // for single-output epilogues: holding two or three weight rows' batches
+    // through the staging takes 226-256 registers, one or two waves a SIMD
+    // (the gate/up dual at M = 1, N = 9728: 10.9 us with PF, 8.6 without)
     const int64_t gy = ceil_div(p.M, mr);
-    const bool pf = mr == 1 && ceil_div(p.Nout, 16) * gy <= 1024 && p.K / 8 <= 512;
+    const bool pf = epi_parts(EPI) == 1 && mr == 1 && ceil_div(p.Nout, 16) * gy <= 1024 &&
+                    p.K / 8 <= 512;
     // A row a wave (LPR 64) for single-output launches over long rows (K >
     // 4096, more than 8 chunks a lane at 16 lanes a row). Waves per workgroup
     // without PF: as many as spread the rows evenly over the CUs in one round
