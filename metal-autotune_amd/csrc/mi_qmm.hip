@@ -380,15 +380,15 @@ constexpr int QV_BATCH = 8;  // 16-byte weight chunks in flight per lane
 
 inline int64_t qmv_dot2_lds_bytes(int mr, int64_t K) { return mr * K * 2 + mr * (K / 32) * 4; }
 
-// A workgroup of blockDim.x / 64 waves owns 4 output rows per wave (16 lanes a
-// row): 4 waves, or for single-output epilogues without PF up to 16 (WIDE),
-// sized by the host so the grid spreads the rows evenly over the CUs. Wider
-// workgroups are not used for the others: batches of two or three weight rows
-// take more than the 128 registers a lane may hold in a 16-wave workgroup,
-// and under PF the staging barriers wait for the x loads of every wave, which
-// queue behind the weight stream (one 10-wave workgroup per CU at N = 9728
-// waited 2.3 us for x against 1.5 us with 4 waves: 6.1 against 5.6 us a
-// launch).
+// A workgroup of blockDim.x / 64 waves owns 64 / LPR output rows per wave (LPR
+// lanes a row, below): 4 waves, or for single-output epilogues without PF up
+// to 16 (WIDE), sized by the host so the grid spreads the rows evenly over the
+// CUs. Wider workgroups are not used for the others: batches of two or three
+// weight rows take more than the 128 registers a lane may hold in a 16-wave
+// workgroup, and under PF the staging barriers wait for the x loads of every
+// wave, which queue behind the weight stream (one 10-wave workgroup per CU at
+// N = 9728 waited 2.3 us for x against 1.5 us with 4 waves: 6.1 against 5.6
+// us a launch).
 // PF (4 waves): the x loads, then the first weight batch, are issued before x
 // is staged, so the weight stream runs under the staging and its two barriers
 // (x first: vmcnt retires in issue order, so waiting for x then leaves the
@@ -953,7 +953,7 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
     const int pitch = p.sbp;
     const SbtLayout tl = {pitch, p.sbninst, p.sbninst * 256};  // sbt_layout(p.kslice, p.gs)
     extern __shared__ __attribute__((aligned(16))) char lds_dyn[];
-    // one scale/bias table per wave, or one for the workgroup (kint)
+    // one scale/bias table per wave, or one for the workgroup (KI)
     static_assert(!KI || (KM == KM_ONE && FH == 1), "interleaved K split: one K part, four waves");
     const char *sbt = lds_dyn + (KI ? 0 : wv) * (A * 2 * tl.array_bytes);
     float *psum = (float *)(lds_dyn + (KI ? 1 : FH * wk) * (A * 2 * tl.array_bytes));  // sums over K parts
@@ -1021,8 +1021,8 @@ __device__ __forceinline__ void qmm_mfma_tile(const QParams &p, char *lds, int64
         // Scale/bias table (layout in sbt_layout): dword v of an array holds
         // groups gbase + 2j, +1 of tile row v / (pitch / 2), j = v % (pitch / 2).
         // Issued before the ring prologue, so the first stage's wait covers it.
-        // kint: one table from group 0, its DMA instructions dealt to the
-        // waves in turn (a barrier after the wait below).
+        // KI: one table from group 0, its DMA instructions dealt to the waves
+        // in turn (a barrier after the wait below).
         const int gbase = KI ? 0 : (kbeg >> gshift) & ~1;
         for (int i = KI ? kw : 0; i < tl.ninst; i += KI ? WK : 1) {
             int v = 64 * i + lane;
