@@ -389,12 +389,13 @@ inline int64_t qmv_dot2_lds_bytes(int mr, int64_t K) { return mr * K * 2 + mr * 
 // wave, which queue behind the weight stream (one 10-wave workgroup per CU at
 // N = 9728 waited 2.3 us for x against 1.5 us with 4 waves: 6.1 against 5.6
 // us a launch).
-// PF (4 waves): the x loads, then the first weight batch, are issued before x
-// is staged, so the weight stream runs under the staging and its two barriers
-// (x first: vmcnt retires in issue order, so waiting for x then leaves the
-// weights in flight). Each thread holds at most two x chunks (MR * K / 8 <=
-// 512). It costs the batch registers through the staging, which pays when
-// the grid fits the chip in one round and not at N = 151936.
+// PF (4 waves at 16 lanes a row; also wide workgroups of a row a wave): the x
+// loads, then the first weight batch, are issued before x is staged, so the
+// weight stream runs under the staging and its two barriers (x first: vmcnt
+// retires in issue order, so waiting for x then leaves the weights in
+// flight). Each thread holds at most two x chunks (K / 8 <= 2 blockDim.x). It
+// costs the batch registers through the staging, which pays when the grid
+// fits the chip in one round and not at N = 151936.
 constexpr bool qmv_dot2_wide_ok(int epi) { return epi_parts(epi) == 1 && epi != EPI_GROUP3; }
 
 // LPR: lanes per output row, 16 (4 rows a wave) or 64 (a row a wave, for long
@@ -402,9 +403,10 @@ constexpr bool qmv_dot2_wide_ok(int epi) { return epi_parts(epi) == 1 && epi != 
 // one after another, and about 5 at 64, one batch).
 template <typename T, int MR, int EPI, bool PF = false, bool WIDE = false, int LPR = 16>
 __global__ __launch_bounds__(WIDE ? 1024 : 256) void qmv_dot2_kernel(QParams p) {
-    static_assert(!WIDE || (!PF && qmv_dot2_wide_ok(EPI)), "wide workgroups: single output, no PF");
-    static_assert(LPR == 16 || (LPR == 64 && !PF && qmv_dot2_wide_ok(EPI)),
-                  "a row a wave: single output, no PF");
+    static_assert(!WIDE || qmv_dot2_wide_ok(EPI), "wide workgroups: single output");
+    static_assert(LPR == 16 || (LPR == 64 && qmv_dot2_wide_ok(EPI)), "a row a wave: single output");
+    static_assert(!PF || MR == 1, "PF: one token");
+    static_assert(!PF || !WIDE || LPR == 64, "PF in wide workgroups: a row a wave");
     constexpr int RPW = 64 / LPR;  // rows a wave
     constexpr int P = epi_parts(EPI);
     typedef Magic<T> Mg;
@@ -458,13 +460,13 @@ __global__ __launch_bounds__(WIDE ? 1024 : 256) void qmv_dot2_kernel(QParams p) 
     };
     const int nw = (int)words;  // 32-bit index math: MR * K < 2^31
     if constexpr (PF) {
-        // 256 threads (4 waves). Every thread issues both loads (a clamped,
-        // valid chunk when past the end) so the issue order, and with it the
-        // waits, is the same in all waves: x, then the weights
+        // Every thread issues both loads (a clamped, valid chunk when past the
+        // end) so the issue order, and with it the waits, is the same in all
+        // waves: x, then the weights (K / 8 <= 2 bs)
         uint4 d[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-            int idx = (int)threadIdx.x + 256 * t;
+            int idx = (int)threadIdx.x + bs * t;
             idx = idx < MR * nw ? idx : MR * nw - 1;
             const int m = MR == 1 ? 0 : idx / nw, w = idx - m * nw;
             d[t] = ld16(x + (int64_t)(m < mr ? m : mr - 1) * K + 8 * w);
@@ -473,7 +475,7 @@ __global__ __launch_bounds__(WIDE ? 1024 : 256) void qmv_dot2_kernel(QParams p) 
         load_batch(j);
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-            const int64_t idx = threadIdx.x + 256 * t;
+            const int64_t idx = threadIdx.x + bs * t;
             if (idx < MR * words) xs_pairs[idx] = pairs(d[t]);
         }
     } else {
@@ -1883,7 +1885,14 @@ int launch_qmv_dot2(const QParams &p, int mr, hipStream_t st) {
         else
             qmv_dot2_kernel<T, 4, EPI><<<grid, bs, lds, st>>>(p);
     } else if constexpr (wide_ok) {
-        if (row_wave && waves == 4) {
+        // a row a wave takes PF too at M = 1 while x fits two chunks a thread
+        // (Qwen3's down_proj at decode, 10-wave workgroups: 6.7 -> 5.6 us)
+        if (row_wave && mr == 1 && p.K / 8 <= 2 * bs) {
+            if (waves == 4)
+                qmv_dot2_kernel<T, 1, EPI, true, false, 64><<<grid, bs, lds, st>>>(p);
+            else
+                qmv_dot2_kernel<T, 1, EPI, true, true, 64><<<grid, bs, lds, st>>>(p);
+        } else if (row_wave && waves == 4) {
             if (mr == 1)
                 qmv_dot2_kernel<T, 1, EPI, false, false, 64><<<grid, bs, lds, st>>>(p);
             else if (mr == 2)
