@@ -19,7 +19,10 @@ Runs, eagerly on the current stream:
    [2560, 4096]^T) and down_proj (x[128, 9728] @ [2560, 9728]^T), each over
    enough weight copies to exceed the Infinity Cache;
 5. the fused q/k/v + q/k-norm + RoPE + cache write (``ops.qkv_norm_rope``,
-   32 q / 8 kv heads of 128 from x[128, 2560]) likewise.
+   32 q / 8 kv heads of 128 from x[128, 2560]) likewise;
+6. the LFM2 prefill's gate/up region: dual 4-bit qmm + SwiGLU at M = 2048
+   (x[2048, 2048] against two [8192, 2048] weights, group 64; the interleaved
+   K split), over enough weight sets to exceed the Infinity Cache.
 
 Prints one line per phase so the counter rows can be matched to phases by
 kernel name and launch order.
@@ -103,6 +106,18 @@ def main():
     torch.cuda.synchronize()
     print(f"phase qkv_norm_rope: {args.reps} x q/k/v + norm + rope M={M} heads {H}+{HK}+{HK} "
           f"D={D} K={K}", flush=True)
+    del wq
+
+    N, K, M = 8192, 2048, 2048
+    sets = 16  # 16 x 2 x 9.4 MB > 256 MB
+    ws = [(random_quantized(N, K, gen, "cuda"), random_quantized(N, K, gen, "cuda"))
+          for _ in range(sets)]
+    x = torch.randn((1, M, K), generator=gen, device="cuda").to(torch.bfloat16)
+    for i in range(args.reps):
+        g, u = ws[i % sets]
+        ops.qmm_dual(x, *g, *u, swiglu=True)
+    torch.cuda.synchronize()
+    print(f"phase dual2048: {args.reps} x qmm_dual swiglu M={M} N=2x{N} K={K}", flush=True)
 
 
 if __name__ == "__main__":
